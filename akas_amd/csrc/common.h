@@ -1,0 +1,222 @@
+// Shared device helpers for the gfx950 block-scaled FP8 path.
+//
+// OCP e4m3 codec, exact float32 quotient, bf16/f16 rounding, dtype-generic
+// loads/stores, the FP8 MFMA wrapper and its fragment layout, and launch
+// helpers.  Everything here is written for CDNA4 (gfx950) wave64.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/akas_fp8.h"
+
+#define AKAS_DEV __device__ __forceinline__
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+namespace akas {
+
+constexpr int kBlock = 128;  // quantization group / weight block edge
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// e4m3 codec
+// ---------------------------------------------------------------------------
+
+// Magnitude code of a non-negative float32, nearest-even, saturating at 126
+// (448).  Normals round the f32 pattern at mantissa bit 20 and rebias by
+// 960 = 120 << 3; magnitudes below 2^-6 are rint(|v| * 512).
+// (src/akas/quantization/_shared/e4m3.py:16-29)
+AKAS_DEV uint32_t e4m3_magnitude_code(float mag) {
+  uint32_t bits = __float_as_uint(mag) & 0x7FFFFFFFu;
+  uint32_t rounded = bits + 0x7FFFFu + ((bits >> 20) & 1u);
+  int normal = (int)(rounded >> 20) - 960;
+  int sub = (int)__builtin_rintf(mag * 512.0f);
+  int code = mag < 0.015625f ? sub : normal;
+  code = code < 0 ? 0 : (code > 126 ? 126 : code);
+  return (uint32_t)code;
+}
+
+// Full encoder: sign of v's bit pattern ORed into the magnitude code.
+AKAS_DEV uint32_t e4m3_encode(float v) {
+  return e4m3_magnitude_code(__builtin_fabsf(v)) | ((__float_as_uint(v) >> 24) & 128u);
+}
+
+// e4m3 byte -> float32 (exact). (src/akas/quantization/_shared/e4m3.py:4-13)
+AKAS_DEV float e4m3_decode(uint32_t b) {
+  uint32_t e = (b >> 3) & 15u, f = b & 7u;
+  uint32_t mag_bits = e ? (((e + 120u) << 23) | (f << 20)) : 0u;
+  float mag = e ? __uint_as_float(mag_bits) : (float)f * (1.0f / 512.0f);
+  return (b & 128u) ? -mag : mag;
+}
+
+// ---------------------------------------------------------------------------
+// exact float32 division by a per-group scale
+// ---------------------------------------------------------------------------
+//
+// The reference divides every element by its group scale with IEEE float32
+// division.  With r = RN(1/s) (one correctly rounded division per group),
+// q0 = RN(x*r), e = x - q0*s (exact through fma) and q = RN(q0 + e*r) is the
+// correctly rounded quotient RN(x/s) for finite, non-underflowing operands
+// (Markstein's correction theorem; Muller et al., Handbook of Floating-Point
+// Arithmetic, ch. 4).  Zero keeps x's sign because callers take the sign bit
+// from x, never from q.
+struct GroupScale {
+  float s;  // the group scale max(max|x|, 1e-12) / 448
+  float r;  // RN(1 / s)
+};
+
+AKAS_DEV GroupScale make_group_scale(float amax) {
+  GroupScale g;
+  g.s = __fdiv_rn(__builtin_fmaxf(amax, 1e-12f), 448.0f);
+  g.r = __fdiv_rn(1.0f, g.s);
+  return g;
+}
+
+AKAS_DEV float exact_quotient_magnitude(float ax, const GroupScale& g) {
+  float q0 = ax * g.r;
+  float e = __builtin_fmaf(-q0, g.s, ax);
+  return __builtin_fmaf(e, g.r, q0);
+}
+
+// enc(RN(x / s)) with the sign taken from x (matches -0.0 / s = -0.0).
+AKAS_DEV uint32_t e4m3_encode_scaled(float x, const GroupScale& g) {
+  float q = exact_quotient_magnitude(__builtin_fabsf(x), g);
+  return e4m3_magnitude_code(q) | ((__float_as_uint(x) >> 24) & 128u);
+}
+
+// ---------------------------------------------------------------------------
+// bf16 / f16 conversions (round to nearest even, finite inputs)
+// ---------------------------------------------------------------------------
+
+AKAS_DEV float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
+
+// (src/akas/quantization/_shared/rounding.py:43-54)
+AKAS_DEV uint32_t f32_to_bf16_bits(float v) {
+  uint32_t bits = __float_as_uint(v);
+  return (bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16;
+}
+
+AKAS_DEV float round_bf16(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+
+AKAS_DEV float f16_bits_to_f32(uint32_t h) {
+  _Float16 x;
+  uint16_t b = (uint16_t)h;
+  __builtin_memcpy(&x, &b, 2);
+  return (float)x;
+}
+
+AKAS_DEV uint32_t f32_to_f16_bits(float v) {
+  _Float16 x = (_Float16)v;  // v_cvt_f16_f32: round to nearest even
+  uint16_t b;
+  __builtin_memcpy(&b, &x, 2);
+  return b;
+}
+
+AKAS_DEV float round_f16(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
+
+AKAS_DEV float round_to(float v, int dtype) {
+  return dtype == AKAS_DTYPE_BF16 ? round_bf16(v) : (dtype == AKAS_DTYPE_F16 ? round_f16(v) : v);
+}
+
+// Element load of a float-like buffer (f32 / f16 / bf16).
+AKAS_DEV float load_elem(const void* p, int64_t i, int dtype) {
+  if (dtype == AKAS_DTYPE_F32) return ((const float*)p)[i];
+  uint32_t h = ((const uint16_t*)p)[i];
+  return dtype == AKAS_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+}
+
+AKAS_DEV void store_elem(void* p, int64_t i, float v, int dtype) {
+  if (dtype == AKAS_DTYPE_F32) {
+    ((float*)p)[i] = v;
+  } else {
+    ((uint16_t*)p)[i] = (uint16_t)(dtype == AKAS_DTYPE_BF16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v));
+  }
+}
+
+// Block-scale element (f32 or bf16 storage).
+AKAS_DEV float load_scale(const void* p, int64_t i, int scale_dtype) {
+  return scale_dtype == AKAS_DTYPE_F32 ? ((const float*)p)[i]
+                                       : bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU element: g / (1 + exp(-g)) * u in float32
+// (src/akas/ops/activation/kernel.py:83-88).  One definition shared by the
+// fused and the separate kernels so their results are bit-identical.
+// ---------------------------------------------------------------------------
+AKAS_DEV float swiglu_elem(float g, float u) {
+  float d = 1.0f + expf(-g);
+  return __fdiv_rn(g, d) * u;
+}
+
+// ---------------------------------------------------------------------------
+// FP8 MFMA: D(16x16, f32) = A(16x128, e4m3) * B(128x16, e4m3)
+// ---------------------------------------------------------------------------
+//
+// Fragment layout used throughout (wave64):
+//   A operand: lane l holds 32 bytes of row (l % 16), k-group g = l / 16,
+//              bytes k = 32*g .. 32*g+31 of the 128-deep block.
+//   B operand: lane l holds the same 32 k-bytes of column (l % 16).
+//   D:         lane l, element i holds row 4*(l/16) + i, column l % 16.
+// The instruction sums matching (lane group, byte) positions of A and B, so
+// any consistent assignment of k to (g, byte) gives the same product; the
+// layout above is verified on the device by tests/test_gpu_mfma_layout.py.
+// The scaled MFMA with unit E8M0 scales (127) is the plain FP8 product;
+// format code 0 selects OCP e4m3 for both operands.
+AKAS_DEV v4f mfma_e4m3(const v8i& a, const v8i& b) {
+  v4f z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 127, 0, 127);
+}
+
+AKAS_DEV v4f mfma_e4m3_acc(const v8i& a, const v8i& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// ---------------------------------------------------------------------------
+// wave reductions
+// ---------------------------------------------------------------------------
+AKAS_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+AKAS_DEV int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Inclusive prefix sum across the 64 lanes.
+AKAS_DEV int wave_inclusive_scan(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// launch helpers
+// ---------------------------------------------------------------------------
+
+// gfx950 dispatches consecutive workgroups round-robin over its 8 XCDs, each
+// with a private L2.  Remap the hardware id so that consecutive logical tiles
+// land on the same XCD (and share its L2) while every XCD gets an equal share.
+AKAS_DEV int xcd_remap(int hw_id, int total) {
+  constexpr int kXcd = 8;
+  int per = total / kXcd;
+  if (per == 0 || hw_id >= per * kXcd) return hw_id;
+  return (hw_id % kXcd) * per + hw_id / kXcd;
+}
+
+}  // namespace akas
+
+// Host-side status helpers.
+#define AKAS_CHECK_LAUNCH()                              \
+  do {                                                   \
+    if (hipGetLastError() != hipSuccess) return AKAS_ERR_LAUNCH; \
+  } while (0)

@@ -1,0 +1,352 @@
+// Dense block-scaled FP8 linear for gfx950: small-M (decode) and LDS-tiled
+// (prefill) MFMA kernels, split-K partials and the partition merge.
+#include "gemm_core.h"
+
+namespace akas {
+
+struct DenseArgs {
+  const uint8_t* a;   // activation codes [M, K]
+  const float* as;    // activation scales [M, K/128]
+  const uint8_t* w;   // weight codes [N, K]
+  const void* ws;     // weight block scales [ceil(N/128), K/128]
+  void* out;
+  int64_t ldo;          // row stride of out, elements
+  int64_t part_stride;  // element offset between partitions of out
+  int M, N, K;
+  int kb_per_part;      // k-blocks per partition
+  int ws_dtype, out_dtype;
+};
+
+// Logical tile id -> (tm, tn): groups of G m-tiles walked n-major so that a
+// window of concurrently running workgroups shares both A and B tiles.
+AKAS_DEV void grouped_tile(int id, int tiles_m, int tiles_n, int G, int& tm, int& tn) {
+  const int per_group = G * tiles_n;
+  const int group = id / per_group, first = group * G;
+  const int gsize = min(tiles_m - first, G);
+  const int local = id % per_group;
+  tm = first + local % gsize;
+  tn = local / gsize;
+}
+
+// ---------------------------------------------------------------------------
+// LDS-tiled MFMA GEMM (prefill shapes and medium M)
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WAVES_M, int WAVES_N, int OUT>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void dense_tiled_kernel(DenseArgs p) {
+  constexpr int THREADS = 64 * WAVES_M * WAVES_N;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int MT = WM / 16, NT = WN / 16;
+  static_assert(128 % WN == 0, "a wave's columns must stay inside one scale block");
+  using Plan = StagePlan<BM, BN, THREADS>;
+  constexpr int STAGE = (BM + BN) * 128;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) float lds_as[2][BM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+  const int id = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+  int tm, tn;
+  grouped_tile(id, tiles_m, tiles_n, 8, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int part = blockIdx.y;
+  const int KB = p.K / kBlock;
+  const int kb0 = part * p.kb_per_part, kb1 = kb0 + p.kb_per_part;
+
+  Plan plan;
+  {
+    const int row = tid >> 3, ch = tid & 7;
+#pragma unroll
+    for (int i = 0; i < Plan::CA; ++i) {
+      const int gm = min(m0 + row + i * Plan::RSTEP, p.M - 1);
+      plan.a_off[i] = (uint32_t)gm * (uint32_t)p.K + ch * 16;
+    }
+    plan.a_base = p.a;
+    plan.b_base = p.w;
+    plan.b_off = (uint32_t)(n0 + row) * (uint32_t)p.K + ch * 16;
+    plan.b_step = (uint32_t)Plan::RSTEP * (uint32_t)p.K;
+    plan.dst0 = lds_off(row, ch);
+  }
+  // Rows past M read row M-1's scales; their outputs are never stored.
+  const float* as_row = p.as + (int64_t)min(m0 + (tid < BM ? tid : 0), p.M - 1) * KB;
+
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int a_row0 = wm * WM, b_row0 = wn * WN;
+  const int wcol = n0 + b_row0;
+  const int64_t ws_base = (int64_t)(wcol / kBlock) * KB;
+
+  Acc<MT, NT> acc;
+  acc.clear();
+  uint4 r[Plan::CA + Plan::CB];
+  float ras = 0.f;
+
+  plan.fetch(kb0, r);
+  ras = as_row[kb0];
+  plan.stash(lds, r);
+  if (tid < BM) lds_as[0][tid] = ras;
+  __syncthreads();
+
+  // The prefetch is unconditional (the last iteration re-reads its own block
+  // into the idle stage) so the staging registers never live in scratch.
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int cur = (kb - kb0) & 1;
+    const int nxt = min(kb + 1, kb1 - 1);
+    plan.fetch(nxt, r);
+    ras = as_row[nxt];
+    const float ws = load_scale(p.ws, ws_base + kb, p.ws_dtype);
+    mma_stage<MT, NT>(acc, lds + cur * STAGE, lds + cur * STAGE + BM * 128, lds_as[cur], a_row0,
+                      b_row0, ws, lane);
+    plan.stash(lds + (cur ^ 1) * STAGE, r);
+    if (tid < BM) lds_as[cur ^ 1][tid] = ras;
+    __syncthreads();
+  }
+
+  const int64_t obase = (int64_t)part * p.part_stride;
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = m0 + a_row0 + 16 * i + 4 * (lane >> 4) + e;
+        const int col = wcol + 16 * j + (lane & 15);
+        if (row < p.M && col < p.N) store_out<OUT>(p.out, obase + (int64_t)row * p.ldo + col, acc.t[i][j][e]);
+      }
+}
+
+// ---------------------------------------------------------------------------
+// Small-M MFMA GEMM: one 16-column tile per workgroup, four waves striding
+// over the k-blocks with every operand fetched straight from global memory
+// (weights stream once from HBM, activations hit L2), then a fixed-order
+// LDS reduction of the four partial tiles.
+// ---------------------------------------------------------------------------
+template <int MT, int OUT>
+__global__ __launch_bounds__(256) void dense_small_kernel(DenseArgs p) {
+  constexpr int U = MT <= 2 ? 4 : 2;  // k-blocks in flight per wave
+  __shared__ __attribute__((aligned(16))) float red[4][MT][64][4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, r16 = lane & 15;
+  const int n0 = blockIdx.x * 16;
+  const int part = blockIdx.y;
+  const int KB = p.K / kBlock;
+  const int kb0 = part * p.kb_per_part, kb1 = kb0 + p.kb_per_part;
+
+  const uint8_t* wrow = p.w + (int64_t)(n0 + r16) * p.K + g * 32;
+  const uint8_t* arow[MT];
+  const float* srow[MT][4];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int m = 16 * i + r16;
+    arow[i] = m < p.M ? p.a + (int64_t)m * p.K + g * 32 : nullptr;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int mo = 16 * i + 4 * g + e;
+      srow[i][e] = mo < p.M ? p.as + (int64_t)mo * KB : nullptr;
+    }
+  }
+  const int64_t ws_base = (int64_t)(n0 / kBlock) * KB;
+
+  v4f acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  for (int kb = kb0 + wave; kb < kb1; kb += 4 * U) {
+    uint4 wl[U][2], al[U][MT][2];
+    float sv[U][MT][4], wsv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = kb + 4 * u;
+      if (k < kb1) {
+        const int64_t ko = (int64_t)k * kBlock;
+        wl[u][0] = *reinterpret_cast<const uint4*>(wrow + ko);
+        wl[u][1] = *reinterpret_cast<const uint4*>(wrow + ko + 16);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          if (arow[i]) {
+            al[u][i][0] = *reinterpret_cast<const uint4*>(arow[i] + ko);
+            al[u][i][1] = *reinterpret_cast<const uint4*>(arow[i] + ko + 16);
+          } else {
+            al[u][i][0] = al[u][i][1] = make_uint4(0, 0, 0, 0);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sv[u][i][e] = srow[i][e] ? srow[i][e][k] : 0.f;
+        }
+        wsv[u] = load_scale(p.ws, ws_base + k, p.ws_dtype);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = kb + 4 * u;
+      if (k < kb1) {
+        v8i bf;
+        bf[0] = wl[u][0].x; bf[1] = wl[u][0].y; bf[2] = wl[u][0].z; bf[3] = wl[u][0].w;
+        bf[4] = wl[u][1].x; bf[5] = wl[u][1].y; bf[6] = wl[u][1].z; bf[7] = wl[u][1].w;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          v8i af;
+          af[0] = al[u][i][0].x; af[1] = al[u][i][0].y; af[2] = al[u][i][0].z; af[3] = al[u][i][0].w;
+          af[4] = al[u][i][1].x; af[5] = al[u][i][1].y; af[6] = al[u][i][1].z; af[7] = al[u][i][1].w;
+          const v4f pr = mfma_e4m3(af, bf);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[i][e] = __builtin_fmaf(pr[e], sv[u][i][e] * wsv[u], acc[i][e]);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+    *reinterpret_cast<float4*>(&red[wave][i][lane][0]) =
+        make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+  __syncthreads();
+  // wave w finalizes m-tiles w, w+4, ... ; fixed summation order 0..3
+  const int64_t obase = (int64_t)part * p.part_stride;
+  for (int i = wave; i < MT; i += 4) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v = red[0][i][lane][e];
+      v += red[1][i][lane][e];
+      v += red[2][i][lane][e];
+      v += red[3][i][lane][e];
+      const int row = 16 * i + 4 * g + e, col = n0 + r16;
+      if (row < p.M) store_out<OUT>(p.out, obase + (int64_t)row * p.ldo + col, v);
+    }
+  }
+}
+
+// Serial f32 sum over partitions (src/akas/ops/linear/cuda.py:1369-1402).
+__global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ partial,
+                                                    void* __restrict__ out, int out_dtype,
+                                                    int64_t rows, int64_t o, int parts) {
+  const int64_t n = rows * o;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / o, col = i % o;
+    const float* src = partial + row * parts * o + col;
+    float t = 0.f;
+    for (int q = 0; q < parts; ++q) t += src[(int64_t)q * o];
+    store_elem(out, i, t, out_dtype);
+  }
+}
+
+template <int BM, int BN, int WMW, int WNW, int OUT>
+static void launch_tiled(const DenseArgs& a, int parts, hipStream_t s) {
+  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  dense_tiled_kernel<BM, BN, WMW, WNW, OUT><<<dim3(tiles, parts), 64 * WMW * WNW, 0, s>>>(a);
+}
+
+// Kernel choice by shape: the direct-load small-M kernel up to 64 rows;
+// beyond that LDS-tiled 256x256 tiles when they fill the GPU, 128x128
+// otherwise.  Tiled kernels need N to be a multiple of their BN (B rows are
+// addressed affinely); other N fall back to 64-row slices of the small kernel.
+template <int OUT>
+static void launch_small(const DenseArgs& a, int parts, hipStream_t s) {
+  if (a.M <= 16)
+    dense_small_kernel<1, OUT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
+  else if (a.M <= 32)
+    dense_small_kernel<2, OUT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
+  else
+    dense_small_kernel<4, OUT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
+}
+
+template <int OUT>
+static void launch_dense_t(const DenseArgs& a, int parts, hipStream_t s) {
+  if (a.M <= 64) {
+    launch_small<OUT>(a, parts, s);
+  } else if (a.N % 128 == 0 && (int64_t)((a.M + 255) / 256) * (a.N / 128) >= 512) {
+    launch_tiled<256, 128, 4, 2, OUT>(a, parts, s);
+  } else if (a.N % 128 == 0) {
+    launch_tiled<128, 128, 2, 2, OUT>(a, parts, s);
+  } else {
+    const int esz = OUT == AKAS_DTYPE_F32 ? 4 : 2;
+    for (int m0 = 0; m0 < a.M; m0 += 64) {
+      DenseArgs b = a;
+      b.M = min(64, a.M - m0);
+      b.a = a.a + (int64_t)m0 * a.K;
+      b.as = a.as + (int64_t)m0 * (a.K / kBlock);
+      b.out = reinterpret_cast<char*>(a.out) + (int64_t)m0 * a.ldo * esz;
+      launch_small<OUT>(b, parts, s);
+    }
+  }
+}
+
+int launch_dense(const DenseArgs& a, int parts, hipStream_t s) {
+  switch (a.out_dtype) {
+    case AKAS_DTYPE_F32: launch_dense_t<AKAS_DTYPE_F32>(a, parts, s); break;
+    case AKAS_DTYPE_BF16: launch_dense_t<AKAS_DTYPE_BF16>(a, parts, s); break;
+    default: launch_dense_t<AKAS_DTYPE_F16>(a, parts, s);
+  }
+  return hipGetLastError() == hipSuccess ? AKAS_OK : AKAS_ERR_LAUNCH;
+}
+
+static inline bool float_dtype(int d) {
+  return d == AKAS_DTYPE_F32 || d == AKAS_DTYPE_F16 || d == AKAS_DTYPE_BF16;
+}
+static inline bool scale_dtype_ok(int d) { return d == AKAS_DTYPE_F32 || d == AKAS_DTYPE_BF16; }
+static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+}  // namespace akas
+
+using namespace akas;
+
+extern "C" size_t akas_fp8_linear_workspace_size(int64_t r, int64_t k, int64_t o) {
+  (void)o;
+  if (r <= 0 || k <= 0) return 0;
+  return align256((size_t)r * k) + align256((size_t)r * (k / kBlock) * sizeof(float));
+}
+
+extern "C" int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const void* w_scales,
+                               int scale_dtype, void* out, int out_dtype, void* workspace,
+                               size_t workspace_bytes, int64_t r, int64_t k, int64_t o,
+                               void* stream) {
+  if (r < 0 || k <= 0 || o <= 0 || k % kBlock || o % 16 || r > 0x7FFFFFFF || o > 0x7FFFFFFF ||
+      k > 0x7FFFFFFF)
+    return AKAS_ERR_GEOMETRY;
+  if (!float_dtype(x_dtype) || !float_dtype(out_dtype) || !scale_dtype_ok(scale_dtype))
+    return AKAS_ERR_DTYPE;
+  if ((uint64_t)r * k >= (1ull << 32) || (uint64_t)o * k >= (1ull << 32)) return AKAS_ERR_GEOMETRY;
+  if (r == 0) return AKAS_OK;
+  if (!x || !w || !w_scales || !out) return AKAS_ERR_NULL;
+  if (!workspace || workspace_bytes < akas_fp8_linear_workspace_size(r, k, o))
+    return AKAS_ERR_WORKSPACE;
+  uint8_t* codes = reinterpret_cast<uint8_t*>(workspace);
+  float* scales = reinterpret_cast<float*>(codes + align256((size_t)r * k));
+  int st = akas_quantize(x, x_dtype, codes, scales, r, k, stream);
+  if (st != AKAS_OK) return st;
+  DenseArgs a{codes, scales, w, w_scales, out, o, 0, (int)r, (int)o, (int)k,
+              (int)(k / kBlock), scale_dtype, out_dtype};
+  return launch_dense(a, 1, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int akas_projection_partial(const uint8_t* x, const float* activation_scales,
+                                       const uint8_t* w, const void* w_scales, int scale_dtype,
+                                       void* out, int out_dtype, int64_t r, int64_t k, int64_t o,
+                                       int partitions, void* stream) {
+  if (r < 0 || k <= 0 || o <= 0 || k % kBlock || o % 16 || partitions < 1 ||
+      (k / kBlock) % partitions || r > 0x7FFFFFFF || o > 0x7FFFFFFF || k > 0x7FFFFFFF)
+    return AKAS_ERR_GEOMETRY;
+  if (!float_dtype(out_dtype) || !scale_dtype_ok(scale_dtype)) return AKAS_ERR_DTYPE;
+  if (partitions > 1 && out_dtype != AKAS_DTYPE_F32) return AKAS_ERR_DTYPE;
+  if ((uint64_t)r * k >= (1ull << 32) || (uint64_t)o * k >= (1ull << 32)) return AKAS_ERR_GEOMETRY;
+  if (r == 0) return AKAS_OK;
+  if (!x || !activation_scales || !w || !w_scales || !out) return AKAS_ERR_NULL;
+  DenseArgs a{x, activation_scales, w, w_scales, out,
+              partitions > 1 ? (int64_t)partitions * o : o, partitions > 1 ? o : 0,
+              (int)r, (int)o, (int)k, (int)(k / kBlock / partitions), scale_dtype, out_dtype};
+  return launch_dense(a, partitions, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int akas_projection_merge(const float* partial, void* out, int out_dtype, int64_t rows,
+                                     int64_t o, int partitions, void* stream) {
+  if (rows < 0 || o <= 0 || partitions < 1) return AKAS_ERR_GEOMETRY;
+  if (!float_dtype(out_dtype)) return AKAS_ERR_DTYPE;
+  if (rows == 0) return AKAS_OK;
+  if (!partial || !out) return AKAS_ERR_NULL;
+  const int64_t n = rows * o;
+  const int64_t want = (n + 255) / 256;
+  const int grid = (int)(want < 16384 ? want : 16384);
+  merge_kernel<<<grid, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(partial, out, out_dtype,
+                                                                        rows, o, partitions);
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}

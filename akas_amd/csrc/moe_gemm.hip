@@ -1,0 +1,380 @@
+// Grouped (per-expert) block-scaled FP8 GEMMs for gfx950:
+//   expert_partial     -- gathered rows x expert weights, scattered to (row, rank)
+//   fp8_expert_swiglu  -- gate and up products in one tile, SwiGLU, and
+//                         per-128-column FP8 re-quantization in the epilogue.
+//
+// Work items are (expert, BM-row tile, BN-column block).  Each workgroup finds
+// its (expert, tile) from a wave-level prefix over ceil(counts[e]/BM), the same
+// enumeration the reference's tile map lists for that row tile
+// (src/akas/ops/moe/kernel.py:79-118), so no host read of counts is needed and
+// the launch stays graph-capturable.  The grid is the reference's capacity
+// bound; surplus workgroups exit at once.
+//
+// Both kernels accumulate every (row, column) in one f32 register in ascending
+// k-block order with acc = fma(P, as*ws, acc), so the fused gate/up values are
+// bit-identical to two expert_partial calls and the fused codes to
+// expert_partial x2 -> swiglu_experts -> quantize.
+#include "gemm_core.h"
+
+namespace akas {
+
+struct ExpertArgs {
+  const uint8_t* x;    // activation codes: [r, k], [r*top, k] (routed) or packed rows
+  const float* as;     // activation scales, same row indexing, k/128 per row
+  const uint8_t* w;    // [E, N, K] codes (gate for the paired kernel)
+  const void* ws;      // [E, NB, KB] block scales
+  const uint8_t* w2;   // up codes (paired)
+  const void* ws2;     // up block scales (paired)
+  const int32_t* counts;
+  const int32_t* routes;   // [E, r]
+  const int32_t* offsets;  // expert_offsets (packed input/output)
+  void* out;
+  float* out_scales;
+  int r, top, E, N, K;
+  int x_rows;    // rows addressable in x / as (gathered rows are clamped to it)
+  int out_rows;  // rows addressable in out (r*top, or packed rows)
+  int routed, packed_in, packed_out;
+  int parts, kb_per_part;
+  int ws_dtype, prod_dtype, act_dtype;
+  int max_tiles, tiles_n;
+};
+
+// (expert, tile) of logical tile t; expert = -1 when t is past the last tile.
+AKAS_DEV void locate_tile(const int32_t* counts, int experts, int bm, int t, int lane,
+                          int& expert, int& tile) {
+  int base = 0;
+  expert = -1;
+  tile = 0;
+  for (int e0 = 0; e0 < experts; e0 += 64) {
+    const int e = e0 + lane;
+    const int c = e < experts ? counts[e] : 0;
+    const int n = ((c > 0 ? c : 0) + bm - 1) / bm;
+    const int incl = wave_inclusive_scan(n, lane);
+    const int excl = incl - n;
+    const uint64_t hit = __ballot(t >= base + excl && t < base + incl);
+    if (hit) {
+      const int src = __builtin_ctzll(hit);
+      expert = e0 + src;
+      tile = t - base - __shfl(excl, src, 64);
+      return;
+    }
+    base += __shfl(incl, 63, 64);
+  }
+}
+
+// Source row of tile row `idx` of expert e in the activation buffer, clamped
+// into the buffer (a corrupt route can only misroute, never fault).
+AKAS_DEV int source_row(const ExpertArgs& p, int e, int idx) {
+  int row;
+  if (p.packed_in) {
+    row = p.offsets[e] + idx;
+  } else {
+    const int route = p.routes[(int64_t)e * p.r + idx];
+    row = p.routed ? route : route / p.top;
+  }
+  return row < 0 ? 0 : (row >= p.x_rows ? p.x_rows - 1 : row);
+}
+
+// MODE 0: expert_partial (scatter f32/f16/bf16 to out[route][part][col]).
+// MODE 1: fp8_expert_swiglu (B tile = 16-row gate/up tiles interleaved).
+template <int BM, int BN, int WAVES_M, int WAVES_N, int MODE, int OUT>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(ExpertArgs p) {
+  constexpr int THREADS = 64 * WAVES_M * WAVES_N;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int MT = WM / 16, NT = WN / 16;
+  constexpr bool PAIRED = MODE == 1;
+  static_assert(!PAIRED || (BN == 256 && NT % 2 == 0), "paired tiles hold 128 gate + 128 up");
+  static_assert(PAIRED || 128 % WN == 0, "a wave's columns must stay inside one scale block");
+  using Plan = StagePlan<BM, BN, THREADS>;
+  constexpr int STAGE = (BM + BN) * 128;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) float lds_as[2][BM];
+  __shared__ int rows_src[BM];
+  __shared__ int rows_dst[BM];
+  __shared__ float row_max[PAIRED ? WAVES_N : 1][PAIRED ? BM : 1];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int id = xcd_remap(blockIdx.x, p.max_tiles * p.tiles_n);
+  const int t = id % p.max_tiles, nb = id / p.max_tiles;
+  int e, tile;
+  locate_tile(p.counts, p.E, BM, t, lane, e, tile);
+  if (e < 0) return;  // uniform across the workgroup
+  const int count = min(p.counts[e], p.r);
+  const int row0 = tile * BM;
+  if (row0 >= count) return;  // only reachable with counts[e] > r
+  const int n0 = nb * (PAIRED ? BN / 2 : BN);
+  const int part = blockIdx.y;
+  const int KB = p.K / kBlock, NB = (p.N + kBlock - 1) / kBlock;
+  const int kb0 = part * p.kb_per_part, kb1 = kb0 + p.kb_per_part;
+
+  // Gathered source rows and scatter destinations of this tile.
+  for (int i = tid; i < BM; i += THREADS) {
+    const int idx = row0 + i;
+    const bool live = idx < count;
+    rows_src[i] = source_row(p, e, live ? idx : row0);
+    int dst = -1;
+    if (live) dst = p.packed_out ? p.offsets[e] + idx : p.routes[(int64_t)e * p.r + idx];
+    rows_dst[i] = dst < p.out_rows ? dst : -1;
+  }
+  __syncthreads();
+
+  Plan plan;
+  {
+    const int row = tid >> 3, ch = tid & 7;
+#pragma unroll
+    for (int i = 0; i < Plan::CA; ++i)
+      plan.a_off[i] = (uint32_t)rows_src[row + i * Plan::RSTEP] * (uint32_t)p.K + ch * 16;
+    plan.a_base = p.x;
+    const int64_t ebase = (int64_t)e * p.N * p.K;
+    if constexpr (PAIRED) {
+      // B row rho: 16-row tile j = rho/16 is gate (even j) or up (odd j)
+      // column n0 + (rho/32)*16 + rho%16; the parity is fixed per thread.
+      const bool up = (row >> 4) & 1;
+      plan.b_base = (up ? p.w2 : p.w) + ebase;
+      plan.b_off = (uint32_t)(n0 + (row >> 5) * 16 + (row & 15)) * (uint32_t)p.K + ch * 16;
+      plan.b_step = (uint32_t)(Plan::RSTEP / 2) * (uint32_t)p.K;
+    } else {
+      plan.b_base = p.w + ebase;
+      plan.b_off = (uint32_t)(n0 + row) * (uint32_t)p.K + ch * 16;
+      plan.b_step = (uint32_t)Plan::RSTEP * (uint32_t)p.K;
+    }
+    plan.dst0 = lds_off(row, ch);
+  }
+  const float* as_row = p.as + (int64_t)rows_src[tid < BM ? tid : 0] * KB;
+
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+  const int a_row0 = wm * WM, b_row0 = wn * WN;
+  // Scale block of this wave's columns (gate and up share it when paired).
+  const int wcol = PAIRED ? n0 + b_row0 / 2 : n0 + b_row0;
+  const int64_t ws_base = ((int64_t)e * NB + wcol / kBlock) * KB;
+
+  Acc<MT, NT> acc;
+  acc.clear();
+  uint4 r[Plan::CA + Plan::CB];
+  float ras;
+  plan.fetch(kb0, r);
+  ras = as_row[kb0];
+  plan.stash(lds, r);
+  if (tid < BM) lds_as[0][tid] = ras;
+  __syncthreads();
+
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int cur = (kb - kb0) & 1;
+    const int nxt = min(kb + 1, kb1 - 1);
+    plan.fetch(nxt, r);
+    ras = as_row[nxt];
+    const float ws0 = load_scale(p.ws, ws_base + kb, p.ws_dtype);
+    const float ws1 = PAIRED ? load_scale(p.ws2, ws_base + kb, p.ws_dtype) : 0.f;
+    mma_stage<MT, NT, PAIRED>(acc, lds + cur * STAGE, lds + cur * STAGE + BM * 128, lds_as[cur],
+                              a_row0, b_row0, ws0, lane, ws1);
+    plan.stash(lds + (cur ^ 1) * STAGE, r);
+    if (tid < BM) lds_as[cur ^ 1][tid] = ras;
+    __syncthreads();
+  }
+
+  if constexpr (!PAIRED) {
+    const int64_t rstride = (int64_t)p.parts * p.N;
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int lr = a_row0 + 16 * i + 4 * (lane >> 4) + e4;
+        const int dst = rows_dst[lr];
+        if (dst < 0) continue;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const int col = wcol + 16 * j + (lane & 15);
+          store_out<OUT>(p.out, (int64_t)dst * rstride + (int64_t)part * p.N + col,
+                         acc.t[i][j][e4]);
+        }
+      }
+  } else {
+    // SwiGLU on (gate, up) pairs held by the same lane, then row max over the
+    // 128 activation columns of the tile (16 lanes x NT/2 tiles x WAVES_N).
+    float act[MT][NT / 2][4];
+    float rmax[MT][4];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        float m = 0.f;
+#pragma unroll
+        for (int j = 0; j < NT / 2; ++j) {
+          const float g = round_to(acc.t[i][2 * j][e4], p.prod_dtype);
+          const float u = round_to(acc.t[i][2 * j + 1][e4], p.prod_dtype);
+          const float a = round_to(swiglu_elem(g, u), p.act_dtype);
+          act[i][j][e4] = a;
+          m = __builtin_fmaxf(m, __builtin_fabsf(a));
+        }
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o, 16));
+        rmax[i][e4] = m;
+      }
+    if ((lane & 15) == 0) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) row_max[wn][a_row0 + 16 * i + 4 * (lane >> 4) + e4] = rmax[i][e4];
+    }
+    __syncthreads();
+    uint8_t* codes = reinterpret_cast<uint8_t*>(p.out);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int lr = a_row0 + 16 * i + 4 * (lane >> 4) + e4;
+        float m = row_max[0][lr];
+#pragma unroll
+        for (int w = 1; w < WAVES_N; ++w) m = __builtin_fmaxf(m, row_max[w][lr]);
+        const GroupScale gs = make_group_scale(m);
+        const int dst = rows_dst[lr];
+        if (dst < 0) continue;
+#pragma unroll
+        for (int j = 0; j < NT / 2; ++j) {
+          const int col = wcol + 16 * j + (lane & 15);
+          codes[(int64_t)dst * p.N + col] = (uint8_t)e4m3_encode_scaled(act[i][j][e4], gs);
+        }
+        if (wn == 0 && (lane & 15) == 0) p.out_scales[(int64_t)dst * (p.N / kBlock) + n0 / kBlock] = gs.s;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launch
+// ---------------------------------------------------------------------------
+
+int64_t capacity_tiles(int64_t r, int64_t top, int64_t experts, int64_t bm) {
+  const int64_t routes = r * top;
+  const int64_t b = (routes + bm - 1) / bm + experts - 1;
+  return routes < b ? routes : b;
+}
+
+template <int BM, int BN, int WMW, int WNW, int MODE, int OUT>
+static void launch_expert(ExpertArgs a, hipStream_t s) {
+  a.max_tiles = (int)capacity_tiles(a.r, a.top, a.E, BM);
+  a.tiles_n = MODE == 1 ? a.N / (BN / 2) : a.N / BN;
+  dim3 grid((unsigned)(a.max_tiles * a.tiles_n), (unsigned)a.parts);
+  expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT><<<grid, 64 * WMW * WNW, 0, s>>>(a);
+}
+
+// Row tile by the mean rows per expert: 32-row tiles for decode-like batches,
+// 128-row tiles once experts hold hundreds of rows.
+template <int OUT>
+static void launch_partial(const ExpertArgs& a, hipStream_t s) {
+  const int64_t mean = (int64_t)a.r * a.top / a.E;
+  if (mean <= 48)
+    launch_expert<32, 128, 1, 4, 0, OUT>(a, s);
+  else
+    launch_expert<128, 128, 2, 2, 0, OUT>(a, s);
+}
+
+static void launch_swiglu(const ExpertArgs& a, hipStream_t s) {
+  const int64_t mean = (int64_t)a.r * a.top / a.E;
+  if (mean <= 48)
+    launch_expert<32, 256, 1, 4, 1, AKAS_DTYPE_F32>(a, s);
+  else
+    launch_expert<128, 256, 2, 4, 1, AKAS_DTYPE_F32>(a, s);
+}
+
+static inline bool float_dtype(int d) {
+  return d == AKAS_DTYPE_F32 || d == AKAS_DTYPE_F16 || d == AKAS_DTYPE_BF16;
+}
+static inline bool scale_dtype_ok(int d) { return d == AKAS_DTYPE_F32 || d == AKAS_DTYPE_BF16; }
+static inline bool valid_block(int m) {
+  return m == 4 || m == 8 || m == 16 || m == 32 || m == 64 || m == 128;
+}
+
+static int check_common(int64_t r, int top, int experts, int64_t o, int64_t k, int max_block_m,
+                        int packed, int64_t x_rows) {
+  if (r < 0 || top < 1 || experts < 1 || experts > 1024 || o <= 0 || k <= 0 || o % kBlock ||
+      k % kBlock || !valid_block(max_block_m))
+    return AKAS_ERR_GEOMETRY;
+  if (r * top > 0x7FFFFFFF || o > 0x7FFFFFFF || k > 0x7FFFFFFF) return AKAS_ERR_GEOMETRY;
+  if ((uint64_t)x_rows * (uint64_t)k >= (1ull << 32)) return AKAS_ERR_GEOMETRY;
+  if ((uint64_t)o * (uint64_t)k >= (1ull << 32)) return AKAS_ERR_GEOMETRY;
+  (void)packed;
+  return AKAS_OK;
+}
+
+}  // namespace akas
+
+using namespace akas;
+
+extern "C" int akas_expert_partial(const uint8_t* x, const float* activation_scales,
+                                   const uint8_t* w, const void* w_scales, int scale_dtype,
+                                   const int32_t* counts, const int32_t* routes,
+                                   const int32_t* tile_experts, const int32_t* tile_offsets,
+                                   const int32_t* expert_offsets, void* out, int out_dtype,
+                                   int64_t r, int top, int experts, int64_t o, int64_t k,
+                                   int routed_input, int partitions, int max_block_m,
+                                   int packed_input, void* stream) {
+  (void)tile_experts;
+  (void)tile_offsets;
+  const int64_t x_rows = packed_input ? capacity_tiles(r, top, experts, max_block_m) * max_block_m
+                                      : (routed_input ? r * top : r);
+  int st = check_common(r, top, experts, o, k, max_block_m, packed_input, x_rows);
+  if (st != AKAS_OK) return st;
+  if (partitions < 1 || (k / kBlock) % partitions) return AKAS_ERR_GEOMETRY;
+  if (!float_dtype(out_dtype) || !scale_dtype_ok(scale_dtype)) return AKAS_ERR_DTYPE;
+  if (partitions > 1 && out_dtype != AKAS_DTYPE_F32) return AKAS_ERR_DTYPE;
+  if (r == 0) return AKAS_OK;
+  if (!x || !activation_scales || !w || !w_scales || !counts || !routes || !out)
+    return AKAS_ERR_NULL;
+  if (packed_input && !expert_offsets) return AKAS_ERR_NULL;
+  ExpertArgs a{};
+  a.x = x; a.as = activation_scales; a.w = w; a.ws = w_scales;
+  a.counts = counts; a.routes = routes; a.offsets = expert_offsets; a.out = out;
+  a.r = (int)r; a.top = top; a.E = experts; a.N = (int)o; a.K = (int)k;
+  a.routed = routed_input; a.packed_in = packed_input; a.packed_out = 0;
+  a.x_rows = (int)x_rows; a.out_rows = (int)(r * top);
+  a.parts = partitions; a.kb_per_part = (int)(k / kBlock / partitions);
+  a.ws_dtype = scale_dtype;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (out_dtype) {
+    case AKAS_DTYPE_F32: launch_partial<AKAS_DTYPE_F32>(a, s); break;
+    case AKAS_DTYPE_BF16: launch_partial<AKAS_DTYPE_BF16>(a, s); break;
+    default: launch_partial<AKAS_DTYPE_F16>(a, s);
+  }
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_fp8_expert_swiglu(const uint8_t* x, const float* activation_scales,
+                                      const uint8_t* w, const void* w_scales, const uint8_t* w2,
+                                      const void* w2_scales, int scale_dtype,
+                                      const int32_t* counts, const int32_t* routes,
+                                      const int32_t* tile_experts, const int32_t* tile_offsets,
+                                      const int32_t* expert_offsets, uint8_t* out,
+                                      float* output_scales, int64_t r, int top, int experts,
+                                      int64_t o, int64_t k, int product_dtype,
+                                      int activation_dtype, int max_block_m, int packed_input,
+                                      int packed_output, void* stream) {
+  (void)tile_experts;
+  (void)tile_offsets;
+  const int64_t x_rows =
+      packed_input ? capacity_tiles(r, top, experts, max_block_m) * max_block_m : r;
+  int st = check_common(r, top, experts, o, k, max_block_m, packed_input, x_rows);
+  if (st != AKAS_OK) return st;
+  if (packed_output && !packed_input) return AKAS_ERR_GEOMETRY;
+  if (!float_dtype(product_dtype) || !float_dtype(activation_dtype) || !scale_dtype_ok(scale_dtype))
+    return AKAS_ERR_DTYPE;
+  if (r == 0) return AKAS_OK;
+  if (!x || !activation_scales || !w || !w_scales || !w2 || !w2_scales || !counts || !routes ||
+      !out || !output_scales)
+    return AKAS_ERR_NULL;
+  if ((packed_input || packed_output) && !expert_offsets) return AKAS_ERR_NULL;
+  ExpertArgs a{};
+  a.x = x; a.as = activation_scales; a.w = w; a.ws = w_scales; a.w2 = w2; a.ws2 = w2_scales;
+  a.counts = counts; a.routes = routes; a.offsets = expert_offsets;
+  a.out = out; a.out_scales = output_scales;
+  a.r = (int)r; a.top = top; a.E = experts; a.N = (int)o; a.K = (int)k;
+  a.routed = 0; a.packed_in = packed_input; a.packed_out = packed_output;
+  a.x_rows = (int)x_rows;
+  a.out_rows = (int)(packed_output ? capacity_tiles(r, top, experts, max_block_m) * max_block_m
+                                   : r * top);
+  a.parts = 1; a.kb_per_part = (int)(k / kBlock);
+  a.ws_dtype = scale_dtype; a.prod_dtype = product_dtype; a.act_dtype = activation_dtype;
+  launch_swiglu(a, reinterpret_cast<hipStream_t>(stream));
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}

@@ -1,0 +1,441 @@
+// Expert routing, stable route compaction, tile maps, expert packing, the
+// expert-row SwiGLU and the weighted top-k combine for gfx950.
+//
+// Everything that fixes a permutation (top-k ids, routes, tile maps, pack
+// offsets) is integer or exact-compare work and is bit-exact by construction:
+// selection compares IEEE float32 scores with lowest-index tie breaking and
+// the route compaction is an ordered block scan, never an atomic cursor.
+#include "common.h"
+
+namespace akas {
+
+// ---------------------------------------------------------------------------
+// routers: one wave per token row
+// ---------------------------------------------------------------------------
+
+// (score, index) arg-max across the wave: larger score wins, ties -> lower index.
+AKAS_DEV void wave_argmax(float& s, int& idx) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float os = __shfl_xor(s, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (os > s || (os == s && oi < idx)) {
+      s = os;
+      idx = oi;
+    }
+  }
+}
+
+constexpr int kMaxExpertSlots = 16;  // experts <= 64 * 16 = 1024
+constexpr int kMaxTop = 32;
+
+// Iterative top-k by maximum with lowest-index ties
+// (src/akas/ops/moe/kernel.py:176-193, :467-483).
+template <int SOFTMAX>
+__global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ logits,
+                                                     const float* __restrict__ bias,
+                                                     int32_t* __restrict__ ids,
+                                                     float* __restrict__ weights, int64_t rows,
+                                                     int experts, int top, float scale,
+                                                     int normalize) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* l = logits + row * experts;
+  float score[kMaxExpertSlots];
+  const int slots = (experts + 63) / 64;
+#pragma unroll
+  for (int s = 0; s < kMaxExpertSlots; ++s) {
+    const int e = s * 64 + lane;
+    float v = -__builtin_inff();
+    if (s < slots && e < experts) {
+      const float b = bias ? bias[e] : 0.f;
+      if (SOFTMAX)
+        v = l[e] + b;
+      else
+        v = __fdiv_rn(1.0f, 1.0f + expf(-l[e])) + b;
+    }
+    score[s] = v;
+  }
+  float chosen[kMaxTop];
+  int chosen_id[kMaxTop];
+  for (int rank = 0; rank < top; ++rank) {
+    float best = -__builtin_inff();
+    int bi = 0x7FFFFFFF;
+    // slots ascend in expert index, so strict > keeps the lowest index on ties
+#pragma unroll
+    for (int s = 0; s < kMaxExpertSlots; ++s) {
+      const int e = s * 64 + lane;
+      if (s < slots && e < experts && (score[s] > best || bi == 0x7FFFFFFF)) {
+        best = score[s];
+        bi = e;
+      }
+    }
+    wave_argmax(best, bi);
+    chosen_id[rank] = bi;
+    if ((bi & 63) == lane) {
+#pragma unroll
+      for (int s = 0; s < kMaxExpertSlots; ++s)
+        if (s == (bi >> 6)) score[s] = -__builtin_inff();
+    }
+    const float lv = l[bi];
+    chosen[rank] = SOFTMAX ? lv : __fdiv_rn(1.0f, 1.0f + expf(-lv));
+  }
+  if (lane == 0) {
+    if (SOFTMAX) {
+      float peak = chosen[0];
+      for (int i = 1; i < top; ++i) peak = __builtin_fmaxf(peak, chosen[i]);
+      float total = 0.f;
+      for (int i = 0; i < top; ++i) total += expf(chosen[i] - peak);
+      for (int i = 0; i < top; ++i) {
+        ids[row * top + i] = chosen_id[i];
+        weights[row * top + i] = __fdiv_rn(scale * expf(chosen[i] - peak), total);
+      }
+    } else {
+      float den = normalize ? 1e-6f : 1.0f;
+      if (normalize)
+        for (int i = 0; i < top; ++i) den += chosen[i];
+      for (int i = 0; i < top; ++i) {
+        ids[row * top + i] = chosen_id[i];
+        weights[row * top + i] = __fdiv_rn(chosen[i] * scale, den);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// quantized_routes: one 1024-thread workgroup per expert, ordered block scan
+// over the rows (src/akas/ops/moe/kernel.py:121-151, cuda.py:2187-2322)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void routes_kernel(const int32_t* __restrict__ ids,
+                                                      const int32_t* __restrict__ active,
+                                                      int32_t* __restrict__ counts,
+                                                      int32_t* __restrict__ routes, int64_t rows,
+                                                      int top) {
+  __shared__ int wave_tot[16];
+  const int e = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int32_t* out = routes + (int64_t)e * rows;
+  int64_t base = 0;
+  for (int64_t r0 = 0; r0 < rows; r0 += 1024) {
+    const int64_t row = r0 + tid;
+    int cnt = 0;
+    if (row < rows && active[row] != 0) {
+      for (int k = 0; k < top; ++k) cnt += ids[row * top + k] == e;
+    }
+    const int incl = wave_inclusive_scan(cnt, lane);
+    if (lane == 63) wave_tot[wave] = incl;
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      const int t = wave_tot[w];
+      before += w < wave ? t : 0;
+      total += t;
+    }
+    if (cnt) {
+      int64_t pos = base + before + incl - cnt;
+      for (int k = 0; k < top; ++k)
+        if (ids[row * top + k] == e) {
+          if (pos < rows) out[pos] = (int32_t)(row * top + k);
+          ++pos;
+        }
+    }
+    base += total;
+    __syncthreads();
+  }
+  const int64_t used = base < rows ? base : rows;
+  for (int64_t i = used + tid; i < rows; i += 1024) out[i] = -1;
+  // counts never exceed the routes row length (only reachable with duplicate
+  // ids in one row, which top-k selection never produces)
+  if (tid == 0) counts[e] = (int32_t)used;
+}
+
+// ---------------------------------------------------------------------------
+// per-expert tile prefix (shared by the tile map and the pack kernel)
+// ---------------------------------------------------------------------------
+
+// prefix[e] = sum_{e' < e} ceil(counts[e'] / tile) (* mult); prefix[E] = total.
+// Computed by wave 0 into LDS; E <= 1024.
+AKAS_DEV void tile_prefix(const int32_t* counts, int experts, int tile, int mult, int* prefix,
+                          int lane) {
+  int carry = 0;
+  for (int e0 = 0; e0 <= experts; e0 += 64) {
+    const int e = e0 + lane;
+    const int c = e < experts ? counts[e] : 0;
+    const int n = ((c > 0 ? c : 0) + tile - 1) / tile * mult;
+    const int incl = wave_inclusive_scan(n, lane);
+    if (e <= experts) prefix[e] = carry + incl - n;
+    carry += __shfl(incl, 63, 64);
+  }
+}
+
+// The expert e with prefix[e] <= p < prefix[e+1] (it is non-empty), for
+// 0 <= p < prefix[experts]; binary search keeps prefix[lo] <= p < prefix[hi].
+AKAS_DEV int find_owner(const int* prefix, int experts, int p) {
+  int lo = 0, hi = experts;  // prefix[lo] <= p < prefix[hi] holds when p < total
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (prefix[mid] <= p)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+// (src/akas/ops/moe/kernel.py:79-118)
+__global__ __launch_bounds__(256) void tile_map_kernel(const int32_t* __restrict__ counts,
+                                                       int32_t* __restrict__ tile_experts,
+                                                       int32_t* __restrict__ tile_rows,
+                                                       int experts, int capacity) {
+  __shared__ int prefix[1025];
+  const int layout = blockIdx.y;
+  const int tile = 4 << layout;
+  if (threadIdx.x < 64) tile_prefix(counts, experts, tile, 1, prefix, threadIdx.x);
+  __syncthreads();
+  const int total = prefix[experts];
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p >= capacity) return;
+  int32_t ex = -1, tr = 0;
+  if (p < total) {
+    ex = find_owner(prefix, experts, p);
+    tr = p - prefix[ex];
+  }
+  tile_experts[(int64_t)layout * capacity + p] = ex;
+  tile_rows[(int64_t)layout * capacity + p] = tr;
+}
+
+// expert_pack: 16 packed rows per 256-thread workgroup, 16 threads per row.
+// (src/akas/ops/moe/cuda.py:2423-2502, oracle validation.py:621-642)
+__global__ __launch_bounds__(256) void pack_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ as,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ routes,
+    uint8_t* __restrict__ packed, float* __restrict__ packed_scales,
+    int32_t* __restrict__ expert_offsets, int64_t rows, int top, int experts, int64_t k,
+    int align, int64_t packed_rows, int routed, int64_t x_rows) {
+  __shared__ int prefix[1025];
+  if (threadIdx.x < 64) tile_prefix(counts, experts, align, align, prefix, threadIdx.x);
+  __syncthreads();
+  const int total = prefix[experts];
+  const int sub = threadIdx.x & 15;
+  const int64_t p = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (p >= total || p >= packed_rows) return;
+  const int e = find_owner(prefix, experts, (int)p);
+  const int local = (int)(p - prefix[e]);
+  const int c = counts[e];
+  const int64_t kb = k / kBlock;
+  if (local == 0 && sub == 0) expert_offsets[e] = prefix[e];
+  uint8_t* dst = packed + p * k;
+  float* dsts = packed_scales + p * kb;
+  const int route = local < c && local < rows ? routes[(int64_t)e * rows + local] : -1;
+  const int64_t src_row = route < 0 ? -1 : (routed ? (int64_t)route : (int64_t)(route / top));
+  if (src_row >= 0 && src_row < x_rows) {
+    const uint8_t* src = x + src_row * k;
+    for (int64_t i = sub * 16; i < k; i += 256)
+      *reinterpret_cast<uint4*>(dst + i) = *reinterpret_cast<const uint4*>(src + i);
+    for (int64_t i = sub; i < kb; i += 16) dsts[i] = as[src_row * kb + i];
+  } else {
+    for (int64_t i = sub * 16; i < k; i += 256)
+      *reinterpret_cast<uint4*>(dst + i) = make_uint4(0, 0, 0, 0);
+    for (int64_t i = sub; i < kb; i += 16) dsts[i] = 1.0f;
+  }
+}
+
+// swiglu_experts (src/akas/ops/activation/kernel.py:28-88)
+__global__ __launch_bounds__(256) void swiglu_kernel(const void* __restrict__ g,
+                                                     const void* __restrict__ u, int in_dtype,
+                                                     void* __restrict__ out, int out_dtype,
+                                                     int64_t rows, int64_t c, int parts,
+                                                     int round_inputs, int round_dtype) {
+  const int64_t n = rows * c;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / c, col = i % c;
+    float gv, uv;
+    if (parts > 1) {
+      gv = 0.f;
+      uv = 0.f;
+      for (int q = 0; q < parts; ++q) {
+        gv += load_elem(g, (row * parts + q) * c + col, in_dtype);
+        uv += load_elem(u, (row * parts + q) * c + col, in_dtype);
+      }
+    } else {
+      gv = load_elem(g, i, in_dtype);
+      uv = load_elem(u, i, in_dtype);
+    }
+    if (round_inputs) {
+      gv = round_to(gv, round_dtype);
+      uv = round_to(uv, round_dtype);
+    }
+    store_elem(out, i, swiglu_elem(gv, uv), out_dtype);
+  }
+}
+
+// routed_combine (src/akas/ops/moe/kernel.py:206-267): 4 columns per thread.
+__global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ experts,
+                                                      int in_dtype,
+                                                      const float* __restrict__ weights,
+                                                      const int32_t* __restrict__ active,
+                                                      float* __restrict__ out, int64_t rows,
+                                                      int top, int64_t c) {
+  const int64_t row = blockIdx.y;
+  const int64_t col = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (col >= c) return;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if (!active || active[row] != 0) {
+    for (int k = 0; k < top; ++k) {
+      const float wv = weights[row * top + k];
+      const int64_t base = (row * top + k) * c + col;
+      if (col + 4 <= c && in_dtype == AKAS_DTYPE_F32 && (c & 3) == 0) {
+        const float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(experts) + base);
+        acc[0] = __builtin_fmaf(v.x, wv, acc[0]);
+        acc[1] = __builtin_fmaf(v.y, wv, acc[1]);
+        acc[2] = __builtin_fmaf(v.z, wv, acc[2]);
+        acc[3] = __builtin_fmaf(v.w, wv, acc[3]);
+      } else {
+        for (int j = 0; j < 4; ++j)
+          if (col + j < c) acc[j] = __builtin_fmaf(load_elem(experts, base + j, in_dtype), wv, acc[j]);
+      }
+    }
+  }
+  for (int j = 0; j < 4; ++j)
+    if (col + j < c) out[row * c + col + j] = acc[j];
+}
+
+static inline bool float_dtype(int d) {
+  return d == AKAS_DTYPE_F32 || d == AKAS_DTYPE_F16 || d == AKAS_DTYPE_BF16;
+}
+
+static inline int grid_for(int64_t n, int per = 256, int cap = 16384) {
+  const int64_t want = (n + per - 1) / per;
+  return (int)(want < cap ? (want > 0 ? want : 1) : cap);
+}
+
+// tile_capacity (src/akas/ops/moe/definition.py:9-16)
+int64_t tile_capacity(int64_t rows, int64_t top, int64_t experts, int64_t block_m) {
+  const int64_t routes = rows * top;
+  const int64_t b = (routes + block_m - 1) / block_m + experts - 1;
+  return routes < b ? routes : b;
+}
+
+bool valid_block(int m) { return m == 4 || m == 8 || m == 16 || m == 32 || m == 64 || m == 128; }
+
+}  // namespace akas
+
+using namespace akas;
+
+extern "C" int akas_biased_router(const float* logits, const float* bias, int32_t* ids,
+                                  float* weights, int64_t r, int experts, int top, float scale,
+                                  int normalize, void* stream) {
+  if (r < 0 || experts < 1 || experts > 64 * kMaxExpertSlots || top < 1 || top > experts ||
+      top > kMaxTop)
+    return AKAS_ERR_GEOMETRY;
+  if (r == 0) return AKAS_OK;
+  if (!logits || !ids || !weights) return AKAS_ERR_NULL;
+  router_kernel<0><<<(int)((r + 3) / 4), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      logits, bias, ids, weights, r, experts, top, scale, normalize);
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_biased_softmax_router(const float* logits, const float* bias, int32_t* ids,
+                                          float* weights, int64_t r, int experts, int top,
+                                          float scale, void* stream) {
+  if (r < 0 || experts < 1 || experts > 64 * kMaxExpertSlots || top < 1 || top > experts ||
+      top > kMaxTop)
+    return AKAS_ERR_GEOMETRY;
+  if (r == 0) return AKAS_OK;
+  if (!logits || !ids || !weights) return AKAS_ERR_NULL;
+  router_kernel<1><<<(int)((r + 3) / 4), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      logits, bias, ids, weights, r, experts, top, scale, 1);
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_quantized_routes(const int32_t* ids, const int32_t* active, int32_t* counts,
+                                     int32_t* routes, int64_t r, int experts, int top,
+                                     void* stream) {
+  if (r < 0 || experts < 1 || top < 1 || r * top > 0x7FFFFFFF) return AKAS_ERR_GEOMETRY;
+  if (!counts || (r > 0 && (!ids || !active || !routes))) return AKAS_ERR_NULL;
+  routes_kernel<<<experts, 1024, 0, reinterpret_cast<hipStream_t>(stream)>>>(ids, active, counts,
+                                                                            routes, r, top);
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_expert_tile_map(const int32_t* counts, int32_t* tile_experts,
+                                    int32_t* tile_rows, int64_t r, int experts, int top,
+                                    int max_block_m, void* stream) {
+  if (r < 0 || experts < 1 || experts > 1024 || top < 1 || !valid_block(max_block_m))
+    return AKAS_ERR_GEOMETRY;
+  if (!counts || !tile_experts || !tile_rows) return AKAS_ERR_NULL;
+  const int layouts = 32 - __builtin_clz((unsigned)max_block_m) - 2;
+  const int64_t capacity = (r * top + 3) / 4 + experts;
+  if (capacity > 0x7FFFFFFF) return AKAS_ERR_GEOMETRY;
+  dim3 grid((unsigned)((capacity + 255) / 256), (unsigned)layouts);
+  tile_map_kernel<<<grid, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      counts, tile_experts, tile_rows, experts, (int)capacity);
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_expert_pack(const uint8_t* x, const float* activation_scales,
+                                const int32_t* counts, const int32_t* routes,
+                                const int32_t* tile_experts, const int32_t* tile_offsets,
+                                uint8_t* packed, float* packed_scales, int32_t* expert_offsets,
+                                int64_t r, int top, int experts, int64_t k, int max_block_m,
+                                int routed_input, void* stream) {
+  (void)tile_experts;
+  (void)tile_offsets;
+  if (r < 1 || top < 1 || experts < 1 || experts > 1024 || k <= 0 || k % kBlock ||
+      !valid_block(max_block_m))
+    return AKAS_ERR_GEOMETRY;
+  if (!x || !activation_scales || !counts || !routes || !packed || !packed_scales ||
+      !expert_offsets)
+    return AKAS_ERR_NULL;
+  const int64_t packed_rows = tile_capacity(r, top, experts, max_block_m) * max_block_m;
+  if (packed_rows > 0x7FFFFFFF) return AKAS_ERR_GEOMETRY;
+  pack_kernel<<<(int)((packed_rows + 15) / 16), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      x, activation_scales, counts, routes, packed, packed_scales, expert_offsets, r, top, experts,
+      k, max_block_m, packed_rows, routed_input, routed_input ? r * top : r);
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_swiglu_experts(const void* g, const void* u, int input_dtype, void* out,
+                                   int output_dtype, int64_t r, int top, int64_t c,
+                                   int partitions, int round_inputs, int round_dtype,
+                                   void* stream) {
+  if (r < 0 || top < 1 || c <= 0 || partitions < 1) return AKAS_ERR_GEOMETRY;
+  if (!float_dtype(input_dtype) || !float_dtype(output_dtype) ||
+      (round_inputs && !float_dtype(round_dtype)))
+    return AKAS_ERR_DTYPE;
+  if (r == 0) return AKAS_OK;
+  if (!g || !u || !out) return AKAS_ERR_NULL;
+  const int64_t rows = r * top;
+  swiglu_kernel<<<grid_for(rows * c), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      g, u, input_dtype, out, output_dtype, rows, c, partitions, round_inputs, round_dtype);
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_routed_combine(const void* experts, int input_dtype, const float* weights,
+                                   const int32_t* active, float* out, int64_t r, int top,
+                                   int64_t c, void* stream) {
+  if (r < 0 || top < 1 || c <= 0 || r > 65535 * 64) return AKAS_ERR_GEOMETRY;
+  if (!float_dtype(input_dtype)) return AKAS_ERR_DTYPE;
+  if (r == 0) return AKAS_OK;
+  if (!experts || !weights || !out) return AKAS_ERR_NULL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  for (int64_t r0 = 0; r0 < r; r0 += 65535) {
+    const int64_t rr = r - r0 < 65535 ? r - r0 : 65535;
+    dim3 grid((unsigned)((c + 1023) / 1024), (unsigned)rr);
+    const size_t esz = input_dtype == AKAS_DTYPE_F32 ? 4 : 2;
+    combine_kernel<<<grid, 256, 0, s>>>(
+        reinterpret_cast<const char*>(experts) + r0 * top * c * esz, input_dtype,
+        weights + r0 * top, active ? active + r0 : nullptr, out + r0 * c, rr, top, c);
+  }
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}

@@ -1,0 +1,94 @@
+"""The routed MoE block over block-FP8 experts, composed from the operator kinds.
+
+Mirrors ``routed_moe`` (src/akas/ops/moe/definition.py:29-201) and the
+policy rewrites that the LFM2-MoE decode/prefill programs use
+(``fused_swiglu``, ``packed``, bf16 intermediate dtypes;
+src/akas/ops/moe/definition.py:442-540, 677-793, 951-1053):
+
+    router -> quantized_routes -> expert_tile_map -> quantize(x)
+      [-> expert_pack] -> fp8_expert_swiglu (or expert_partial x2 ->
+      swiglu_experts -> quantize) -> expert_partial(down, routed_input)
+      -> routed_combine
+"""
+
+from dataclasses import dataclass
+
+import torch
+
+from . import ops
+
+
+@dataclass
+class ExpertWeights:
+    """Block-FP8 expert banks: gate ``w1``/up ``w3`` ``[E, F, H]`` and down
+    ``w2`` ``[E, H, F]`` with 128x128 block scales (f32 or bf16)."""
+
+    w1: torch.Tensor
+    s1: torch.Tensor
+    w3: torch.Tensor
+    s3: torch.Tensor
+    w2: torch.Tensor
+    s2: torch.Tensor
+
+    @property
+    def experts(self):
+        return self.w1.shape[0]
+
+    @property
+    def hidden(self):
+        return self.w1.shape[2]
+
+    @property
+    def width(self):
+        return self.w1.shape[1]
+
+
+def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
+               router="biased_softmax_router", scale=1.0, normalize=True, fused_swiglu=True,
+               packed=False, max_block_m=64, product_dtype=torch.float32,
+               activation_dtype=torch.float32, contribution_dtype=torch.float32,
+               return_routing=False):
+    """One routed MoE feed-forward: ``x [T, H]`` (f32/f16/bf16) -> f32 ``[T, H]``."""
+    if router not in ("biased_router", "biased_softmax_router"):
+        raise ValueError("unknown routed expert scoring")
+    if packed and not fused_swiglu:
+        raise ValueError("packing requires the fused SwiGLU pair kernel")
+    rows, hidden = x.shape
+    experts = weights.experts
+    if active is None:
+        active = torch.ones(rows, dtype=torch.int32, device=x.device)
+    if router == "biased_router":
+        ids, probability = ops.biased_router(logits, bias, top=top, scale=scale,
+                                             normalize=normalize)
+    else:
+        ids, probability = ops.biased_softmax_router(logits, bias, top=top, scale=scale)
+    counts, routes = ops.quantized_routes(ids, active, experts=experts)
+    tile_experts, tile_rows = ops.expert_tile_map(counts, r=rows, top=top,
+                                                  max_block_m=max_block_m)
+    codes, scales = ops.quantize(x)
+    common = dict(r=rows, top=top, max_block_m=max_block_m)
+    offsets = None
+    if packed:
+        codes, scales, offsets = ops.expert_pack(codes, scales, counts, routes, tile_experts,
+                                                 tile_rows, top=top, max_block_m=max_block_m)
+    if fused_swiglu:
+        act, act_scales = ops.fp8_expert_swiglu(
+            codes, scales, weights.w1, weights.s1, weights.w3, weights.s3, counts, routes,
+            tile_experts, tile_rows, offsets, product_dtype=product_dtype,
+            activation_dtype=activation_dtype, packed_input=packed, packed_output=packed,
+            **common)
+    else:
+        gate = ops.expert_partial(codes, scales, weights.w1, weights.s1, counts, routes,
+                                  tile_experts, tile_rows, output_dtype=product_dtype, **common)
+        up = ops.expert_partial(codes, scales, weights.w3, weights.s3, counts, routes,
+                                tile_experts, tile_rows, output_dtype=product_dtype, **common)
+        activated = ops.swiglu_experts(gate, up, output_dtype=activation_dtype)
+        act, act_scales = ops.quantize(activated, top=top)
+    contributions = ops.expert_partial(
+        act, act_scales, weights.w2, weights.s2, counts, routes, tile_experts, tile_rows,
+        offsets, routed_input=not packed, packed_input=packed, output_dtype=contribution_dtype,
+        **common)
+    out = ops.routed_combine(contributions, probability, active)
+    if return_routing:
+        return out, dict(ids=ids, weights=probability, counts=counts, routes=routes)
+    return out

@@ -1,0 +1,445 @@
+"""Operator kinds of the block-scaled FP8 path, on PyTorch-ROCm device tensors.
+
+Each function mirrors one graph call kind of the reference (same name, same
+parameter meaning, same buffer names and output order) and calls the gfx950
+C ABI of ``include/akas_fp8.h`` on the current HIP stream.  Outputs may be
+passed in (caller-owned buffers, as in the reference runtime) or are
+allocated here with torch.  Invalid geometry raises ``ValueError`` before any
+launch, like the reference factories.  There is no CPU fallback.
+"""
+
+import torch
+
+from . import _lib
+from ._lib import BF16, F16, F32, check
+
+BLOCK = 128
+
+_DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+_NAME_TO_TORCH = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+
+
+def _dt(dtype):
+    """torch dtype or reference dtype name -> ABI code."""
+    if isinstance(dtype, str):
+        dtype = _NAME_TO_TORCH.get(dtype)
+    if dtype not in _DTYPE_CODE:
+        raise ValueError(f"unsupported dtype {dtype}")
+    return _DTYPE_CODE[dtype]
+
+
+def _torch_dtype(dtype):
+    return _NAME_TO_TORCH[dtype] if isinstance(dtype, str) else dtype
+
+
+def _stream():
+    """hipStream_t of torch's current stream on the current device."""
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _need(t, name, dtype=None, shape=None, device=None):
+    if t is None:
+        raise ValueError(f"{name} is required")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype not in (dtype if isinstance(dtype, tuple) else (dtype,)):
+        raise ValueError(f"{name} has dtype {t.dtype}, expected {dtype}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    return t
+
+
+def _out(t, name, shape, dtype, like):
+    if t is None:
+        return torch.empty(shape, dtype=dtype, device=like.device)
+    return _need(t, name, dtype, shape)
+
+
+_FLOATS = (torch.float32, torch.float16, torch.bfloat16)
+_SCALES = (torch.float32, torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# activation / weight codecs
+# ---------------------------------------------------------------------------
+
+def quantize(x, *, top=None, out=None, scales=None):
+    """``quantize(r, k[, top, input_dtype]): x -> out, scales``.
+
+    ``x``: f32/f16/bf16 ``[r, k]`` or ``[r, top, k]``.  Returns e4m3 codes
+    (uint8, same shape) and f32 scales ``[..., k/128]``.
+    (src/akas/quantization/activations/fp8/cuda.py:10-56)
+    """
+    _need(x, "x", _FLOATS)
+    if top is not None and (x.dim() != 3 or x.shape[1] != top):
+        raise ValueError("routed quantize input must be [r, top, k]")
+    k = x.shape[-1]
+    if k % BLOCK:
+        raise ValueError("FP8 channels must be divisible by 128")
+    rows = x.numel() // k
+    out = _out(out, "out", tuple(x.shape), torch.uint8, x)
+    scales = _out(scales, "scales", (*x.shape[:-1], k // BLOCK), torch.float32, x)
+    check(_lib.load().akas_quantize(_ptr(x), _dt(x.dtype), _ptr(out), _ptr(scales), rows, k,
+                                    _stream()), "quantize")
+    return out, scales
+
+
+def dequantize_fp8(codes, scales, *, out=None, out_dtype=torch.float32):
+    """``dequantize_fp8``: ``decode(codes) * scale`` per 128-group."""
+    _need(codes, "codes", torch.uint8)
+    k = codes.shape[-1]
+    _need(scales, "scales", torch.float32, (*codes.shape[:-1], k // BLOCK))
+    out = _out(out, "out", tuple(codes.shape), _torch_dtype(out_dtype), codes)
+    check(_lib.load().akas_dequantize_fp8(_ptr(codes), _ptr(scales), _ptr(out), _dt(out.dtype),
+                                          codes.numel() // k, k, _stream()), "dequantize_fp8")
+    return out
+
+
+def quantize_weight_blocks(w, *, scale_dtype=torch.float32):
+    """Block-quantize f32 weights ``[(E,) n, k]`` to e4m3 codes and 128x128 scales.
+
+    Device form of the reference's host weight preparation
+    (src/akas/quantization/weights/fp8/kernel.py:34-59).
+    """
+    _need(w, "w", torch.float32)
+    n, k = w.shape[-2:]
+    if k % BLOCK:
+        raise ValueError("FP8 weight channels must be divisible by 128")
+    batch = w.numel() // (n * k) if n * k else 0
+    codes = torch.empty(w.shape, dtype=torch.uint8, device=w.device)
+    scales = torch.empty((*w.shape[:-2], (n + BLOCK - 1) // BLOCK, k // BLOCK),
+                         dtype=_torch_dtype(scale_dtype), device=w.device)
+    check(_lib.load().akas_quantize_weight_blocks(_ptr(w), _ptr(codes), _ptr(scales),
+                                                  _dt(scales.dtype), batch, n, k, _stream()),
+          "quantize_weight_blocks")
+    return codes, scales
+
+
+# ---------------------------------------------------------------------------
+# dense linear
+# ---------------------------------------------------------------------------
+
+_WORKSPACES = {}
+
+
+def linear_workspace(r, k, o, device):
+    """Cached, zero-filled workspace for :func:`fp8_linear` (per device)."""
+    need = _lib.load().akas_fp8_linear_workspace_size(r, k, o)
+    key = torch.device(device).index if torch.device(device).index is not None else \
+        torch.cuda.current_device()
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def fp8_linear(x, w, scales, *, out=None, out_dtype=torch.float32, workspace=None):
+    """``fp8_linear(r, k, o[, input_dtype]): x, w, scales -> out``.
+
+    ``x`` f32/f16/bf16 ``[r, k]`` is quantized per 1x128 group, multiplied by
+    the e4m3 weight ``[o, k]`` with 128x128 block ``scales`` (f32 or bf16,
+    ``[ceil(o/128), k/128]``), f32 accumulation, stored as ``out_dtype``.
+    (src/akas/ops/linear/cuda.py:642-646, :757-828)
+    """
+    _need(x, "x", _FLOATS)
+    _need(w, "w", torch.uint8)
+    if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
+        raise ValueError("fp8_linear expects x [r, k] and w [o, k]")
+    r, k = x.shape
+    o = w.shape[0]
+    if k % BLOCK or o % 16:
+        raise ValueError("invalid FP8 projection geometry")
+    _need(scales, "scales", _SCALES, ((o + BLOCK - 1) // BLOCK, k // BLOCK))
+    out = _out(out, "out", (r, o), _torch_dtype(out_dtype), x)
+    if workspace is None:
+        workspace = linear_workspace(r, k, o, x.device)
+    check(_lib.load().akas_fp8_linear(
+        _ptr(x), _dt(x.dtype), _ptr(w), _ptr(scales), _dt(scales.dtype), _ptr(out),
+        _dt(out.dtype), _ptr(workspace), workspace.numel(), r, k, o, _stream()), "fp8_linear")
+    return out
+
+
+def projection_partial(x, activation_scales, w, scales, *, partitions=1, out=None,
+                       out_dtype=torch.float32):
+    """``projection_partial(r, k, o, partitions)`` on prequantized codes.
+
+    ``partitions == 1``: ``out [r, o]``; otherwise f32 ``[r, partitions, o]``.
+    (src/akas/ops/linear/cuda.py:649-653)
+    """
+    _need(x, "x", torch.uint8)
+    _need(w, "w", torch.uint8)
+    r, k = x.shape
+    o = w.shape[0]
+    if w.shape[1] != k or k % BLOCK or o % 16 or partitions < 1 or (k // BLOCK) % partitions:
+        raise ValueError("invalid FP8 projection geometry")
+    _need(activation_scales, "activation_scales", torch.float32, (r, k // BLOCK))
+    _need(scales, "scales", _SCALES, ((o + BLOCK - 1) // BLOCK, k // BLOCK))
+    shape = (r, partitions, o) if partitions > 1 else (r, o)
+    dtype = torch.float32 if partitions > 1 else _torch_dtype(out_dtype)
+    out = _out(out, "out", shape, dtype, x)
+    check(_lib.load().akas_projection_partial(
+        _ptr(x), _ptr(activation_scales), _ptr(w), _ptr(scales), _dt(scales.dtype), _ptr(out),
+        _dt(out.dtype), r, k, o, partitions, _stream()), "projection_partial")
+    return out
+
+
+def projection_merge(partial, *, out=None, out_dtype=torch.float32):
+    """``projection_merge(r, o, partitions)``: serial f32 sum over partitions."""
+    _need(partial, "partial", torch.float32)
+    parts, o = partial.shape[-2:]
+    rows = partial.numel() // (parts * o) if parts * o else 0
+    out = _out(out, "out", (*partial.shape[:-2], o), _torch_dtype(out_dtype), partial)
+    check(_lib.load().akas_projection_merge(_ptr(partial), _ptr(out), _dt(out.dtype), rows, o,
+                                            parts, _stream()), "projection_merge")
+    return out
+
+
+def expert_merge(partial, *, out=None, output_dtype=torch.float32):
+    """``expert_merge(r, top, o, partitions)``: ``[r, top, parts, o] -> [r, top, o]``."""
+    if partial.dim() != 4:
+        raise ValueError("expert_merge expects [r, top, partitions, o]")
+    return projection_merge(partial, out=out, out_dtype=output_dtype)
+
+
+# ---------------------------------------------------------------------------
+# routing
+# ---------------------------------------------------------------------------
+
+def biased_router(logits, bias, *, top, scale=1.0, normalize=True, ids=None, weights=None):
+    """``biased_router(r, experts, top, scale, normalize): logits, bias -> ids, weights``.
+
+    (src/akas/ops/moe/kernel.py:154-203)
+    """
+    _need(logits, "logits", torch.float32)
+    r, experts = logits.shape
+    if bias is not None:
+        _need(bias, "bias", torch.float32, (experts,))
+    ids = _out(ids, "ids", (r, top), torch.int32, logits)
+    weights = _out(weights, "weights", (r, top), torch.float32, logits)
+    check(_lib.load().akas_biased_router(_ptr(logits), _ptr(bias), _ptr(ids), _ptr(weights), r,
+                                         experts, top, float(scale), int(bool(normalize)),
+                                         _stream()), "biased_router")
+    return ids, weights
+
+
+def biased_softmax_router(logits, bias, *, top, scale=1.0, ids=None, weights=None):
+    """``biased_softmax_router(r, experts, top, scale)`` (src/akas/ops/moe/kernel.py:444-499)."""
+    _need(logits, "logits", torch.float32)
+    r, experts = logits.shape
+    if bias is not None:
+        _need(bias, "bias", torch.float32, (experts,))
+    ids = _out(ids, "ids", (r, top), torch.int32, logits)
+    weights = _out(weights, "weights", (r, top), torch.float32, logits)
+    check(_lib.load().akas_biased_softmax_router(_ptr(logits), _ptr(bias), _ptr(ids),
+                                                 _ptr(weights), r, experts, top, float(scale),
+                                                 _stream()), "biased_softmax_router")
+    return ids, weights
+
+
+def quantized_routes(ids, active, *, experts, counts=None, routes=None):
+    """``quantized_routes(r, experts, top): ids, active -> counts, routes``.
+
+    (src/akas/ops/moe/kernel.py:121-151)
+    """
+    _need(ids, "ids", torch.int32)
+    r, top = ids.shape
+    _need(active, "active", torch.int32, (r,))
+    counts = _out(counts, "counts", (experts,), torch.int32, ids)
+    routes = _out(routes, "routes", (experts, r), torch.int32, ids)
+    check(_lib.load().akas_quantized_routes(_ptr(ids), _ptr(active), _ptr(counts), _ptr(routes),
+                                            r, experts, top, _stream()), "quantized_routes")
+    return counts, routes
+
+
+def tile_capacity(rows, top, experts, block_m):
+    """Non-empty expert tile bound (src/akas/ops/moe/definition.py:9-16)."""
+    if any(type(v) is not int or v < 1 for v in (rows, top, experts, block_m)):
+        raise ValueError("expert tile geometry must contain positive integers")
+    routes = rows * top
+    return min(routes, (routes + block_m - 1) // block_m + experts - 1)
+
+
+def tile_layouts(max_block_m=64):
+    """Row layouts 4..max_block_m (src/akas/ops/moe/definition.py:19-26)."""
+    if type(max_block_m) is not int or max_block_m not in (4, 8, 16, 32, 64, 128):
+        raise ValueError(
+            "expert maximum row tile must be a supported power of two from 4 through 128")
+    return max_block_m.bit_length() - 2
+
+
+def map_capacity(rows, top, experts):
+    return (rows * top + 3) // 4 + experts
+
+
+def expert_tile_map(counts, *, r, top, max_block_m=64, tile_experts=None, tile_rows=None):
+    """``expert_tile_map(r, experts, top[, max_block_m]): counts -> tile_experts, tile_rows``.
+
+    (src/akas/ops/moe/kernel.py:79-118)
+    """
+    _need(counts, "counts", torch.int32)
+    experts = counts.shape[0]
+    shape = (tile_layouts(max_block_m), map_capacity(r, top, experts))
+    tile_experts = _out(tile_experts, "tile_experts", shape, torch.int32, counts)
+    tile_rows = _out(tile_rows, "tile_rows", shape, torch.int32, counts)
+    check(_lib.load().akas_expert_tile_map(_ptr(counts), _ptr(tile_experts), _ptr(tile_rows), r,
+                                           experts, top, max_block_m, _stream()),
+          "expert_tile_map")
+    return tile_experts, tile_rows
+
+
+def expert_pack(x, activation_scales, counts, routes, tile_experts, tile_offsets, *, top,
+                max_block_m=64, routed_input=False, packed=None, packed_scales=None,
+                expert_offsets=None):
+    """``expert_pack(r, top, experts, k, max_block_m[, routed_input])``.
+
+    Returns ``(packed, packed_scales, expert_offsets)``; padding rows hold codes
+    0 and scale 1 (src/akas/ops/moe/cuda.py:2423-2502).
+    """
+    _need(x, "x", torch.uint8)
+    _need(counts, "counts", torch.int32)
+    experts = counts.shape[0]
+    r = x.shape[0]
+    k = x.shape[-1]
+    if routed_input and (x.dim() != 3 or x.shape[1] != top):
+        raise ValueError("routed pack input must be [r, top, k]")
+    _need(activation_scales, "activation_scales", torch.float32, (*x.shape[:-1], k // BLOCK))
+    _need(routes, "routes", torch.int32, (experts, r))
+    rows = tile_capacity(r, top, experts, max_block_m) * max_block_m
+    packed = _out(packed, "packed", (rows, k), torch.uint8, x)
+    packed_scales = _out(packed_scales, "packed_scales", (rows, k // BLOCK), torch.float32, x)
+    if expert_offsets is None:
+        expert_offsets = torch.zeros((experts,), dtype=torch.int32, device=x.device)
+    _need(expert_offsets, "expert_offsets", torch.int32, (experts,))
+    check(_lib.load().akas_expert_pack(
+        _ptr(x), _ptr(activation_scales), _ptr(counts), _ptr(routes), _ptr(tile_experts),
+        _ptr(tile_offsets), _ptr(packed), _ptr(packed_scales), _ptr(expert_offsets), r, top,
+        experts, k, max_block_m, int(bool(routed_input)), _stream()), "expert_pack")
+    return packed, packed_scales, expert_offsets
+
+
+# ---------------------------------------------------------------------------
+# grouped expert products
+# ---------------------------------------------------------------------------
+
+def expert_partial(x, activation_scales, w, scales, counts, routes, tile_experts=None,
+                   tile_offsets=None, expert_offsets=None, *, r, top, routed_input=False,
+                   partitions=1, output_dtype=torch.float32, max_block_m=64,
+                   packed_input=False, out=None):
+    """``expert_partial``: grouped FP8 projection scattered to ``out[row, rank]``.
+
+    ``out`` is ``[r, top, o]`` (``partitions == 1``) or f32
+    ``[r, top, partitions, o]``; only routed entries are written
+    (src/akas/ops/moe/cuda.py:541-1354).
+    """
+    _need(x, "x", torch.uint8)
+    _need(w, "w", torch.uint8)
+    experts, o, k = w.shape
+    _need(scales, "scales", _SCALES, (experts, (o + BLOCK - 1) // BLOCK, k // BLOCK))
+    _need(counts, "counts", torch.int32, (experts,))
+    _need(routes, "routes", torch.int32, (experts, r))
+    if x.shape[-1] != k:
+        raise ValueError("activation depth differs from the expert weights")
+    _need(activation_scales, "activation_scales", torch.float32, (*x.shape[:-1], k // BLOCK))
+    if packed_input and expert_offsets is None:
+        raise ValueError("packed expert input requires expert_offsets")
+    shape = (r, top, partitions, o) if partitions > 1 else (r, top, o)
+    dtype = torch.float32 if partitions > 1 else _torch_dtype(output_dtype)
+    if out is None:
+        out = torch.zeros(shape, dtype=dtype, device=x.device)
+    _need(out, "out", dtype, shape)
+    check(_lib.load().akas_expert_partial(
+        _ptr(x), _ptr(activation_scales), _ptr(w), _ptr(scales), _dt(scales.dtype), _ptr(counts),
+        _ptr(routes), _ptr(tile_experts), _ptr(tile_offsets), _ptr(expert_offsets), _ptr(out),
+        _dt(out.dtype), r, top, experts, o, k, int(bool(routed_input)), partitions, max_block_m,
+        int(bool(packed_input)), _stream()), "expert_partial")
+    return out
+
+
+def fp8_expert_swiglu(x, activation_scales, w, scales, w2, scales2, counts, routes,
+                      tile_experts=None, tile_offsets=None, expert_offsets=None, *, r, top,
+                      product_dtype=torch.float32, activation_dtype=torch.float32,
+                      max_block_m=64, packed_input=False, packed_output=False, out=None,
+                      output_scales=None):
+    """``fp8_expert_swiglu``: gate/up products, SwiGLU, FP8 re-quantization.
+
+    Returns ``(out, output_scales)``: codes ``[r, top, o]`` and scales
+    ``[r, top, o/128]`` (packed ``[cap*A, ...]`` with ``packed_output``)
+    (src/akas/ops/moe/cuda.py:823-946).
+    """
+    _need(x, "x", torch.uint8)
+    _need(w, "w", torch.uint8)
+    _need(w2, "w2", torch.uint8, tuple(w.shape))
+    experts, o, k = w.shape
+    sshape = (experts, (o + BLOCK - 1) // BLOCK, k // BLOCK)
+    _need(scales, "scales", _SCALES, sshape)
+    _need(scales2, "scales2", scales.dtype, sshape)
+    _need(counts, "counts", torch.int32, (experts,))
+    _need(routes, "routes", torch.int32, (experts, r))
+    _need(activation_scales, "activation_scales", torch.float32, (*x.shape[:-1], k // BLOCK))
+    if (packed_input or packed_output) and expert_offsets is None:
+        raise ValueError("packed experts require expert_offsets")
+    if packed_output and not packed_input:
+        raise ValueError("packed expert output requires a packed paired projection")
+    if packed_output:
+        rows = tile_capacity(r, top, experts, max_block_m) * max_block_m
+        oshape, sshape_out = (rows, o), (rows, o // BLOCK)
+    else:
+        oshape, sshape_out = (r, top, o), (r, top, o // BLOCK)
+    if out is None:
+        out = torch.zeros(oshape, dtype=torch.uint8, device=x.device)
+    if output_scales is None:
+        output_scales = torch.zeros(sshape_out, dtype=torch.float32, device=x.device)
+    _need(out, "out", torch.uint8, oshape)
+    _need(output_scales, "output_scales", torch.float32, sshape_out)
+    check(_lib.load().akas_fp8_expert_swiglu(
+        _ptr(x), _ptr(activation_scales), _ptr(w), _ptr(scales), _ptr(w2), _ptr(scales2),
+        _dt(scales.dtype), _ptr(counts), _ptr(routes), _ptr(tile_experts), _ptr(tile_offsets),
+        _ptr(expert_offsets), _ptr(out), _ptr(output_scales), r, top, experts, o, k,
+        _dt(product_dtype), _dt(activation_dtype), max_block_m, int(bool(packed_input)),
+        int(bool(packed_output)), _stream()), "fp8_expert_swiglu")
+    return out, output_scales
+
+
+def swiglu_experts(g, u, *, round_inputs=False, round_dtype=torch.float32,
+                   output_dtype=torch.float32, out=None):
+    """``swiglu_experts``: ``g / (1 + exp(-g)) * u`` on ``[r, top, (parts,) c]``.
+
+    (src/akas/ops/activation/kernel.py:28-88)
+    """
+    _need(g, "g", _FLOATS)
+    _need(u, "u", g.dtype, tuple(g.shape))
+    if g.dim() == 4:
+        r, top, parts, c = g.shape
+    elif g.dim() == 3:
+        (r, top, c), parts = g.shape, 1
+    else:
+        raise ValueError("expert SwiGLU expects [r, top, c] or [r, top, parts, c]")
+    out = _out(out, "out", (r, top, c), _torch_dtype(output_dtype), g)
+    check(_lib.load().akas_swiglu_experts(
+        _ptr(g), _ptr(u), _dt(g.dtype), _ptr(out), _dt(out.dtype), r, top, c, parts,
+        int(bool(round_inputs)), _dt(round_dtype), _stream()), "swiglu_experts")
+    return out
+
+
+def routed_combine(experts, weights, active, *, out=None):
+    """``routed_combine(r, top, c[, input_dtype]): experts, weights, active -> out``.
+
+    (src/akas/ops/moe/kernel.py:206-267)
+    """
+    _need(experts, "experts", _FLOATS)
+    r, top, c = experts.shape
+    _need(weights, "weights", torch.float32, (r, top))
+    if active is not None:
+        _need(active, "active", torch.int32, (r,))
+    out = _out(out, "out", (r, c), torch.float32, experts)
+    check(_lib.load().akas_routed_combine(_ptr(experts), _dt(experts.dtype), _ptr(weights),
+                                          _ptr(active), _ptr(out), r, top, c, _stream()),
+          "routed_combine")
+    return out

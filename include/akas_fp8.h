@@ -1,0 +1,275 @@
+/*
+ * akas_fp8.h -- C ABI of the MI355X (gfx950) block-scaled FP8 matrix-product
+ * path: FP8 activation quantizer, 128x128 block-scaled linear, expert routing,
+ * permutation, tile maps and packing, grouped expert GEMMs (gate_up with fused
+ * SwiGLU re-quantization, down) and the weighted top-k combine.
+ *
+ * One entry point per operator kind of the reference's graph API.  Each
+ * comment cites the reference interface it replaces (paths relative to the
+ * reference repository root).
+ *
+ * Conventions (all entry points):
+ *   - every pointer is a device pointer on the current HIP device, except
+ *     where noted; dims are passed by value;
+ *   - `stream` is a hipStream_t (0 = the legacy default stream);
+ *   - calls are asynchronous and stream-ordered: no allocation, no host
+ *     synchronization and no host reads of device data happen inside a call,
+ *     so every call can be captured in a HIP graph;
+ *   - geometry, null pointers and dtype codes are validated on the host before
+ *     any launch; the return value is AKAS_OK or a negative AKAS_ERR_* code;
+ *   - distinct streams may call concurrently; calls sharing a workspace must
+ *     be stream-ordered.
+ *
+ * Layouts (row-major, last index fastest):
+ *   activation codes  u8  [rows, k]         scales f32 [rows, k/128]
+ *   weight codes      u8  [(E,) n, k]       scales f32|bf16 [(E,) ceil(n/128), k/128]
+ *   routes            i32 [E, r]  value row*top + rank, padding -1
+ *   tile maps         i32 [layouts, (r*top+3)/4 + E]
+ */
+#ifndef AKAS_FP8_H
+#define AKAS_FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element dtype codes */
+#define AKAS_DTYPE_F32 0
+#define AKAS_DTYPE_F16 1
+#define AKAS_DTYPE_BF16 2
+
+/* status codes */
+#define AKAS_OK 0
+#define AKAS_ERR_GEOMETRY -1 /* invalid shape / tile geometry (reference ValueError) */
+#define AKAS_ERR_NULL -2     /* required pointer is null */
+#define AKAS_ERR_DTYPE -3    /* unsupported dtype code */
+#define AKAS_ERR_LAUNCH -4   /* HIP launch failed */
+#define AKAS_ERR_WORKSPACE -5 /* workspace missing or too small */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int akas_version(void);
+
+/* Static text for a status code. */
+const char* akas_status_string(int status);
+
+/* Number of entry points declared in this header and exported by the library. */
+int akas_abi_count(void);
+
+/* ------------------------------------------------------------------------ */
+/* FP8 activation quantizer                                                  */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * quantize(r, k[, top, input_dtype]): x -> out, scales.
+ * Replaces src/akas/quantization/activations/fp8/cuda.py:10-56 (kind
+ * "quantize", OutputABI (1, 2) at definition.py:43-48).
+ * rows = r * (top or 1); x is f32/f16/bf16 [rows, k]; k % 128 == 0.
+ * scales[g] = max(max|x_g|, 1e-12) / 448; out = e4m3(x / scale), bit-exact.
+ */
+int akas_quantize(const void* x, int x_dtype, uint8_t* out, float* scales,
+                  int64_t rows, int64_t k, void* stream);
+
+/*
+ * dequantize_fp8: codes, scales -> out (f32/f16/bf16) = decode(code) * scale.
+ * Replaces src/akas/quantization/activations/fp8/kernel.py dequantize
+ * (kind "dequantize_fp8", definition.py:43-46, 61-70).
+ */
+int akas_dequantize_fp8(const uint8_t* codes, const float* scales, void* out, int out_dtype,
+                        int64_t rows, int64_t k, void* stream);
+
+/*
+ * Block-quantize f32 weights [batch, n, k] to e4m3 codes and 128x128 block
+ * scales max(max|block|, 1e-12)/448 (rounded to bf16 first when
+ * scale_dtype == AKAS_DTYPE_BF16).  Device equivalent of the host weight
+ * preparation src/akas/quantization/weights/fp8/kernel.py:34-59 with the
+ * storage layout of weights/fp8/definition.py:12-27.
+ */
+int akas_quantize_weight_blocks(const float* w, uint8_t* codes, void* scales, int scale_dtype,
+                                int64_t batch, int64_t n, int64_t k, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Dense block-scaled FP8 linear                                             */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Workspace bytes needed by akas_fp8_linear for (r, k, o): activation codes
+ * and scales (plus split-K partials for small-r launches).  Host-only.
+ */
+size_t akas_fp8_linear_workspace_size(int64_t r, int64_t k, int64_t o);
+
+/*
+ * fp8_linear(r, k, o[, input_dtype]): x, w, scales -> out.
+ * Replaces src/akas/ops/linear/cuda.py:642-646 (fp8_inline, _mma with inline
+ * quantization :102-501) and the r<=8 GEMV native_fp8 (:757-828); kind
+ * registered at src/akas/ops/linear/definition.py:1890-1914.
+ * x f32/f16/bf16 [r, k]; w u8 [o, k]; w_scales f32|bf16 [ceil(o/128), k/128];
+ * out f32/f16/bf16 [r, o] = quantize(x) . dequant(w)^T, f32 accumulation.
+ * k % 128 == 0 and o % 16 == 0.  The workspace must be zero-filled before
+ * its first use; every call leaves it zero-filled again.
+ */
+int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const void* w_scales,
+                    int scale_dtype, void* out, int out_dtype, void* workspace,
+                    size_t workspace_bytes, int64_t r, int64_t k, int64_t o, void* stream);
+
+/*
+ * projection_partial(r, k, o, partitions): prequantized x, w, scales,
+ * activation_scales -> out.
+ * Replaces src/akas/ops/linear/cuda.py:649-653 (fp8_prequantized) and
+ * :452-483; kind at src/akas/ops/linear/definition.py:1304-1321.
+ * partitions == 1: out [r, o] in out_dtype.  partitions > 1: out f32
+ * [r, partitions, o] with partition p summing k-blocks
+ * [p*k/(128*partitions), (p+1)*k/(128*partitions)).
+ */
+int akas_projection_partial(const uint8_t* x, const float* activation_scales, const uint8_t* w,
+                            const void* w_scales, int scale_dtype, void* out, int out_dtype,
+                            int64_t r, int64_t k, int64_t o, int partitions, void* stream);
+
+/*
+ * projection_merge(r, o, partitions) / expert_merge(r, top, o, partitions):
+ * partial f32 [rows, partitions, o] -> out [rows, o] (serial f32 sum).
+ * Replaces src/akas/ops/linear/cuda.py:1369-1402 (kinds projection_merge,
+ * src/akas/ops/linear/definition.py:1322-1328, and expert_merge,
+ * src/akas/ops/moe/definition.py:2409-2420).  rows = r * (top or 1).
+ */
+int akas_projection_merge(const float* partial, void* out, int out_dtype, int64_t rows, int64_t o,
+                          int partitions, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Routing                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * biased_router(r, experts, top, scale, normalize): logits, bias -> ids, weights.
+ * Replaces src/akas/ops/moe/kernel.py:154-203 (kind at
+ * src/akas/ops/moe/definition.py:1946-1971).  Selects on
+ * sigmoid(l) + b (ties -> lowest index); weights = sigmoid(l_sel) * scale /
+ * (sum + 1e-6) when normalize, else sigmoid(l_sel) * scale.
+ * experts <= 1024, top <= experts.
+ */
+int akas_biased_router(const float* logits, const float* bias, int32_t* ids, float* weights,
+                       int64_t r, int experts, int top, float scale, int normalize, void* stream);
+
+/*
+ * biased_softmax_router(r, experts, top, scale): logits, bias -> ids, weights.
+ * Replaces src/akas/ops/moe/kernel.py:444-499 (definition.py:2475-2490).
+ * Selects on logits + bias (ties -> lowest index); weights = scale *
+ * softmax over the selected unbiased logits.
+ */
+int akas_biased_softmax_router(const float* logits, const float* bias, int32_t* ids,
+                               float* weights, int64_t r, int experts, int top, float scale,
+                               void* stream);
+
+/*
+ * quantized_routes(r, experts, top): ids, active -> counts, routes.
+ * Replaces src/akas/ops/moe/kernel.py:121-151 and the parallel variant
+ * src/akas/ops/moe/cuda.py:2187-2322.  Stable (row, rank) order, bit-exact;
+ * routes [experts, r] padded with -1.  Requires each row's ids to hold an
+ * expert at most once (true of top-k ids), so counts[e] <= r.
+ */
+int akas_quantized_routes(const int32_t* ids, const int32_t* active, int32_t* counts,
+                          int32_t* routes, int64_t r, int experts, int top, void* stream);
+
+/*
+ * expert_tile_map(r, experts, top[, max_block_m]): counts -> tile_experts, tile_rows.
+ * Replaces src/akas/ops/moe/kernel.py:79-118 (parallel cuda.py:2095-2175).
+ * Shape [layouts, (r*top+3)/4 + experts] with layouts = log2(max_block_m) - 1
+ * (row tiles 4, 8, ..., max_block_m); padding (-1, 0).
+ */
+int akas_expert_tile_map(const int32_t* counts, int32_t* tile_experts, int32_t* tile_rows,
+                         int64_t r, int experts, int top, int max_block_m, void* stream);
+
+/*
+ * expert_pack(r, top, experts, k, max_block_m[, routed_input]):
+ * x, activation_scales, counts, routes, tile_experts, tile_offsets ->
+ * packed, packed_scales, expert_offsets.
+ * Replaces src/akas/ops/moe/cuda.py:2423-2502 (kind at
+ * src/akas/ops/moe/definition.py:2491-2501).  packed [cap*A, k] with
+ * cap = tile_capacity(r, top, experts, A), A = max_block_m; padding codes 0,
+ * scales 1; expert_offsets written for non-empty experts only.
+ */
+int akas_expert_pack(const uint8_t* x, const float* activation_scales, const int32_t* counts,
+                     const int32_t* routes, const int32_t* tile_experts,
+                     const int32_t* tile_offsets, uint8_t* packed, float* packed_scales,
+                     int32_t* expert_offsets, int64_t r, int top, int experts, int64_t k,
+                     int max_block_m, int routed_input, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Grouped expert GEMMs                                                      */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * expert_partial(r, top, experts, o, k, routed_input, partitions, tile_map
+ * [, max_block_m, output_dtype, packed_input]):
+ * x, activation_scales, w, scales, counts, routes, tile_experts, tile_offsets
+ * [, expert_offsets] -> out.
+ * Replaces src/akas/ops/moe/cuda.py:541-1354 (_bucketed, mapped registration
+ * src/akas/ops/moe/definition.py:2326-2366).
+ *   x: codes [r, k] (or [r, top, k] if routed_input; or packed [cap*A, k]
+ *      when packed_input) with 1x128 activation scales;
+ *   w: [experts, o, k] codes, scales [experts, ceil(o/128), k/128];
+ *   out: [r, top, o] in out_dtype (partitions == 1) or f32
+ *        [r, top, partitions, o]; only routed (row, rank) entries are written.
+ * The tile map is validated for shape; work items are derived on the device
+ * from counts (identical to the map's layout by construction).
+ * o % 128 == 0, k % 128 == 0.
+ */
+int akas_expert_partial(const uint8_t* x, const float* activation_scales, const uint8_t* w,
+                        const void* w_scales, int scale_dtype, const int32_t* counts,
+                        const int32_t* routes, const int32_t* tile_experts,
+                        const int32_t* tile_offsets, const int32_t* expert_offsets, void* out,
+                        int out_dtype, int64_t r, int top, int experts, int64_t o, int64_t k,
+                        int routed_input, int partitions, int max_block_m, int packed_input,
+                        void* stream);
+
+/*
+ * fp8_expert_swiglu(r, top, experts, o, k[, product_dtype, activation_dtype,
+ * max_block_m, packed_input, packed_output]):
+ * x, activation_scales, w, scales, w2, scales2, counts, routes, tile_experts,
+ * tile_offsets[, expert_offsets] -> out, output_scales.
+ * Replaces the paired _bucketed epilogue src/akas/ops/moe/cuda.py:823-946
+ * (kind at src/akas/ops/moe/definition.py:2367-2406, 1861-1863).
+ * g = x.w^T, u = x.w2^T (f32), rounded to product_dtype; a = silu(g)*u
+ * rounded to activation_dtype; per 128 columns s = max(max|a|,1e-12)/448 and
+ * out = e4m3(a/s).  out u8 [r, top, o] (or packed [cap*A, o]), output_scales
+ * f32 [r, top, o/128] (or [cap*A, o/128]).  Bit-identical to expert_partial
+ * x2 -> swiglu_experts -> quantize with the same dtypes.
+ */
+int akas_fp8_expert_swiglu(const uint8_t* x, const float* activation_scales, const uint8_t* w,
+                           const void* w_scales, const uint8_t* w2, const void* w2_scales,
+                           int scale_dtype, const int32_t* counts, const int32_t* routes,
+                           const int32_t* tile_experts, const int32_t* tile_offsets,
+                           const int32_t* expert_offsets, uint8_t* out, float* output_scales,
+                           int64_t r, int top, int experts, int64_t o, int64_t k,
+                           int product_dtype, int activation_dtype, int max_block_m,
+                           int packed_input, int packed_output, void* stream);
+
+/*
+ * swiglu_experts(r, top, c, expert_rows, input_dtype, output_dtype
+ * [, round_inputs, round_dtype, partitions]): g, u -> out.
+ * Replaces src/akas/ops/activation/kernel.py:28-88.  g, u
+ * [r, top, (partitions,) c] in input_dtype; partitions are summed in f32
+ * first; round_inputs rounds g and u to round_dtype; out [r, top, c] =
+ * g / (1 + exp(-g)) * u stored in output_dtype.
+ */
+int akas_swiglu_experts(const void* g, const void* u, int input_dtype, void* out,
+                        int output_dtype, int64_t r, int top, int64_t c, int partitions,
+                        int round_inputs, int round_dtype, void* stream);
+
+/*
+ * routed_combine(r, top, c[, input_dtype]): experts, weights, active -> out.
+ * Replaces src/akas/ops/moe/kernel.py:206-267.  out f32 [r, c] =
+ * sum over rank (serial order) of experts[r, rank, c] * weights[r, rank];
+ * rows with active == 0 are zero.
+ */
+int akas_routed_combine(const void* experts, int input_dtype, const float* weights,
+                        const int32_t* active, float* out, int64_t r, int top, int64_t c,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AKAS_FP8_H */

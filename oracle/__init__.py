@@ -1,0 +1,36 @@
+"""CPU oracle for the block-scaled FP8 matrix-product path.
+
+TEST INFRASTRUCTURE ONLY.  This package restates, in plain NumPy (and in the
+C file ``cpu_ref.c`` next to it), the reference's CPU equations for the FP8
+codec, the 1x128 activation quantizer, the 128x128 block-scaled linear,
+expert routing/permutation/tile maps/packing, the grouped expert products,
+the fused SwiGLU re-quantization and the weighted top-k combine.  Every
+function cites the reference file:line it follows (paths are relative to the
+reference repository root, ``src/akas/...`` or ``tests/...``).
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import, call, link or execute anything in this directory, and
+there only as the checker or the timed CPU baseline.  The product path
+(``akas_amd``) never imports it and has no CPU fallback.
+
+Pinning (what each function is checked against, in ``tests/test_oracle_*.py``):
+
+* ``encode_e4m3`` / ``decode_e4m3``: brute force over every code, an
+  independent nearest-even search over the 253 finite magnitudes, torch's
+  ``float8_e4m3fn`` cast on finite values, and the quantizer stress row of
+  ``src/akas/quantization/activations/fp8/validation.py:24``.
+* ``bf16_round``: torch's ``bfloat16`` cast (round-to-nearest-even).
+* ``quantize``: the stress row known answers and the zero-row scale
+  ``1e-12/448``; closed-form round trip bounds.
+* ``fp8_linear`` and the expert products: exact-product inputs (integer
+  codes with binary scales, ``src/akas/ops/moe/validation.py:327-360``) whose
+  float64 result is exact, linearity in the weight scales, and a per-element
+  brute-force triple loop on tiny shapes.
+* routing, tile maps and packing: brute-force enumerations written
+  independently in the tests (stable argsort, explicit loops), the
+  deterministic route patterns of ``src/akas/ops/moe/validation.py:82-99`` and
+  ``:606-611``, and the empty-batch invariants of ``tests/test_lfm_moe.py``.
+* ``routed_combine``: explicit per-element loop.
+
+No function here is "parity unpinned".
+"""

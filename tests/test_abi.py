@@ -1,0 +1,65 @@
+"""CPU: the C-ABI library loads and exports every entry point of the header."""
+
+import ctypes
+import os
+import re
+
+from akas_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "akas_fp8.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(akas_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_table_agree():
+    assert header_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_header_symbol():
+    lib = ctypes.CDLL(_lib.LIBRARY)  # dlopen only; nothing touches a GPU
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    lib.akas_abi_count.restype = ctypes.c_int
+    assert lib.akas_abi_count() == len(header_functions())
+    lib.akas_status_string.restype = ctypes.c_char_p
+    assert lib.akas_status_string(0) == b"ok"
+    assert lib.akas_status_string(-1) == b"invalid geometry"
+
+
+def test_host_validation_rejects_before_launch():
+    """Invalid geometry returns an error code without touching the device."""
+    lib = _lib.load()
+    # k not a multiple of 128
+    assert lib.akas_quantize(1, 2, 1, 1, 4, 200, None) == -1
+    # bad dtype code
+    assert lib.akas_quantize(1, 7, 1, 1, 4, 256, None) == -3
+    # null pointers with real work
+    assert lib.akas_quantize(None, 2, None, None, 4, 256, None) == -2
+    # zero rows is a no-op
+    assert lib.akas_quantize(None, 2, None, None, 0, 256, None) == 0
+    # linear: o not a multiple of 16, workspace too small
+    assert lib.akas_fp8_linear(1, 2, 1, 1, 0, 1, 0, 1, 1 << 30, 4, 256, 100, None) == -1
+    assert lib.akas_fp8_linear(1, 2, 1, 1, 0, 1, 0, 1, 16, 4, 256, 128, None) == -5
+    # partitions must divide k/128
+    assert lib.akas_projection_partial(1, 1, 1, 1, 0, 1, 0, 4, 384, 128, 2, None) == -1
+    # tile map: unsupported maximum row tile
+    assert lib.akas_expert_tile_map(1, 1, 1, 4, 8, 2, 48, None) == -1
+    # router: top larger than experts
+    assert lib.akas_biased_router(1, 1, 1, 1, 4, 8, 9, 1.0, 1, None) == -1
+    # expert partial: o not a multiple of 128
+    assert lib.akas_expert_partial(1, 1, 1, 1, 0, 1, 1, 1, 1, None, 1, 0, 4, 2, 4, 100, 256,
+                                   0, 1, 64, 0, None) == -1
+    # fused swiglu: packed output without packed input
+    assert lib.akas_fp8_expert_swiglu(1, 1, 1, 1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 4, 2, 4, 128,
+                                      256, 0, 0, 64, 0, 1, None) == -1
+
+
+def test_workspace_size_formula():
+    lib = _lib.load()
+    assert lib.akas_fp8_linear_workspace_size(16, 2048, 6144) == 16 * 2048 + 16 * 16 * 4
+    assert lib.akas_fp8_linear_workspace_size(0, 2048, 6144) == 0

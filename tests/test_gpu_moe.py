@@ -1,0 +1,410 @@
+"""GPU parity: routing, permutation, tile maps, packing, grouped expert GEMMs,
+fused SwiGLU re-quantization and the weighted combine."""
+
+import numpy as np
+import pytest
+
+from oracle import fp8 as ofp8
+from oracle import moe as omoe
+from golden_inputs import bf16_normal, exact_codes, random_codes, rel_fro
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev, dtype=None):
+    import torch
+
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.to(dev)
+
+
+def _np(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy() if t.dtype in (torch.bfloat16, torch.float16) else t.cpu().numpy()
+
+
+def pattern_routes(rows, top, experts, mult=1, inactive_last=True):
+    ids = ((np.arange(rows)[:, None] * mult + np.arange(top)[None, :]) % experts).astype(np.int32)
+    active = np.ones(rows, np.int32)
+    if rows > 1 and inactive_last:
+        active[-1] = 0
+    return ids, active
+
+
+# ---------------------------------------------------------------------------
+# routers
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,experts,top", [(1, 64, 4), (257, 64, 4), (64, 256, 8), (9, 7, 3)])
+def test_softmax_router(dev, rows, experts, top):
+    from akas_amd import ops
+
+    rng = np.random.default_rng(17)
+    logits = rng.normal(0, 1, (rows, experts)).astype(np.float32)
+    bias = rng.normal(0, 0.1, experts).astype(np.float32)
+    logits[0, 1] = logits[0, 0]  # forced tie resolved to the lower id
+    bias[1] = bias[0]
+    ids, w = ops.biased_softmax_router(_t(logits, dev), _t(bias, dev), top=top, scale=1.5)
+    eids, ew = omoe.biased_softmax_router(logits, bias, top, scale=1.5)
+    np.testing.assert_array_equal(_np(ids), eids)
+    np.testing.assert_allclose(_np(w), ew, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("normalize", [True, False])
+def test_sigmoid_router(dev, normalize):
+    from akas_amd import ops
+
+    rng = np.random.default_rng(18)
+    rows, experts, top = 65, 64, 4
+    logits = rng.normal(0, 1, (rows, experts)).astype(np.float32)
+    logits[0] = 0  # exact ties: bias decides, then the lowest id
+    bias = (np.arange(experts)[::-1] % 3 * 0.1).astype(np.float32)
+    ids, w = ops.biased_router(_t(logits, dev), _t(bias, dev), top=top, scale=2.0,
+                               normalize=normalize)
+    eids, ew = omoe.biased_router(logits, bias, top, 2.0, normalize)
+    np.testing.assert_array_equal(_np(ids), eids)
+    np.testing.assert_allclose(_np(w), ew, rtol=2e-6, atol=1e-7)
+
+
+# ---------------------------------------------------------------------------
+# routes / tile map / pack
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,top,experts,mult", [(1, 4, 64, 1), (33, 2, 4, 1), (1025, 4, 64, 3),
+                                                   (16384, 4, 64, 7), (257, 3, 7, 1)])
+def test_quantized_routes_patterns(dev, rows, top, experts, mult):
+    from akas_amd import ops
+
+    ids, active = pattern_routes(rows, top, experts, mult)
+    counts, routes = ops.quantized_routes(_t(ids, dev), _t(active, dev), experts=experts)
+    ec, er = omoe.quantized_routes(ids, active, experts)
+    np.testing.assert_array_equal(_np(counts), ec)
+    np.testing.assert_array_equal(_np(routes), er)
+
+
+def test_quantized_routes_from_router_zipf(dev):
+    """Skewed top-4 routing of 16384 tokens over 64 experts."""
+    from akas_amd import ops
+
+    rng = np.random.default_rng(0)
+    rows, experts, top = 16384, 64, 4
+    logits = rng.normal(0, 1, (rows, experts)).astype(np.float32)
+    logits += (-1.1 * np.log1p(rng.permutation(experts))).astype(np.float32)[None, :]
+    ids, _ = ops.biased_softmax_router(_t(logits, dev), None, top=top)
+    active = np.ones(rows, np.int32)
+    active[rng.random(rows) < 0.05] = 0
+    counts, routes = ops.quantized_routes(ids, _t(active, dev), experts=experts)
+    ec, er = omoe.quantized_routes(_np(ids), active, experts)
+    np.testing.assert_array_equal(_np(counts), ec)
+    np.testing.assert_array_equal(_np(routes), er)
+    assert ec.max() > 3 * ec.mean()  # the skew is real
+
+
+def test_quantized_routes_empty_batch(dev):
+    from akas_amd import ops
+
+    ids, _ = pattern_routes(8, 2, 5)
+    active = np.zeros(8, np.int32)
+    counts, routes = ops.quantized_routes(_t(ids, dev), _t(active, dev), experts=5)
+    assert not _np(counts).any()
+    assert (_np(routes) == -1).all()
+
+
+@pytest.mark.parametrize("rows,top,experts,maxm", [(33, 3, 7, 64), (257, 3, 7, 128), (1, 4, 64, 64),
+                                                   (16384, 4, 64, 128)])
+def test_expert_tile_map(dev, rows, top, experts, maxm):
+    from akas_amd import ops
+
+    ids, active = pattern_routes(rows, top, experts, 3)
+    ec, _ = omoe.quantized_routes(ids, active, experts)
+    te, tr = ops.expert_tile_map(_t(ec, dev), r=rows, top=top, max_block_m=maxm)
+    ete, etr = omoe.expert_tile_map(ec, rows, top, maxm)
+    np.testing.assert_array_equal(_np(te), ete)
+    np.testing.assert_array_equal(_np(tr), etr)
+
+
+@pytest.mark.parametrize("rows,maximum,routed", [(1, 16, False), (33, 64, False), (129, 128, True)])
+def test_expert_pack(dev, rows, maximum, routed):
+    """(src/akas/ops/moe/validation.py:595-618 geometry: k=256, top=3, experts=7)"""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(rows)
+    top, experts, k = 3, 7, 256
+    ids, active = pattern_routes(rows, top, experts, 3)
+    counts, routes = omoe.quantized_routes(ids, active, experts)
+    shape = (rows, top, k) if routed else (rows, k)
+    x = random_codes(rng, shape)
+    xs = rng.uniform(0.0625, 0.25, (*shape[:-1], k // 128)).astype(np.float32)
+    te, tr = omoe.expert_tile_map(counts, rows, top, maximum)
+    cap = omoe.tile_capacity(rows, top, experts, maximum) * maximum
+    packed = torch.zeros((cap, k), dtype=torch.uint8, device=dev)
+    pscales = torch.ones((cap, k // 128), dtype=torch.float32, device=dev)
+    offs = torch.zeros((experts,), dtype=torch.int32, device=dev)
+    ops.expert_pack(_t(x, dev), _t(xs, dev), _t(counts, dev), _t(routes, dev), _t(te, dev),
+                    _t(tr, dev), top=top, max_block_m=maximum, routed_input=routed,
+                    packed=packed, packed_scales=pscales, expert_offsets=offs)
+    ep, es, eo = omoe.expert_pack(x, xs, counts, routes, top, experts, maximum, routed)
+    np.testing.assert_array_equal(_np(packed), ep)
+    np.testing.assert_array_equal(_np(pscales), es)
+    np.testing.assert_array_equal(_np(offs), eo)
+
+
+# ---------------------------------------------------------------------------
+# grouped expert GEMMs
+# ---------------------------------------------------------------------------
+
+def _expert_case(rng, rows, top, experts, o, k, routed, exact=True, mult=1):
+    ids, active = pattern_routes(rows, top, experts, mult)
+    counts, routes = omoe.quantized_routes(ids, active, experts)
+    shape = (rows, top, k) if routed else (rows, k)
+    gen = exact_codes if exact else random_codes
+    x = gen(rng, shape)
+    w = gen(rng, (experts, o, k))
+    if exact:
+        xs = (2.0 ** rng.integers(-4, 1, (*shape[:-1], k // 128))).astype(np.float32)
+        ws = (2.0 ** rng.integers(-4, 1, (experts, o // 128, k // 128))).astype(np.float32)
+    else:
+        xs = rng.uniform(0.0625, 0.25, (*shape[:-1], k // 128)).astype(np.float32)
+        ws = ofp8.bf16_round(rng.uniform(0.0625, 0.25, (experts, o // 128, k // 128)).astype(np.float32))
+    return ids, active, counts, routes, x, xs, w, ws
+
+
+@pytest.mark.parametrize("rows,top,experts,o,k,routed", [
+    (3, 2, 4, 128, 256, False), (1, 4, 64, 128, 256, False), (33, 2, 4, 128, 256, False),
+    (33, 2, 4, 128, 384, True), (257, 3, 7, 256, 384, True), (256, 4, 64, 256, 512, False),
+    (2048, 4, 8, 256, 256, False)])
+def test_expert_partial_exact(dev, rows, top, experts, o, k, routed):
+    from akas_amd import ops
+
+    rng = np.random.default_rng(37)
+    ids, active, counts, routes, x, xs, w, ws = _expert_case(rng, rows, top, experts, o, k, routed)
+    out = ops.expert_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev), _t(counts, dev),
+                             _t(routes, dev), r=rows, top=top, routed_input=routed)
+    exp = omoe.expert_partial(x, xs, w, ws, counts, routes, top, routed_input=routed)
+    np.testing.assert_array_equal(_np(out), exp)
+
+
+@pytest.mark.parametrize("out_dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("scale_dtype", ["float32", "bfloat16"])
+def test_expert_partial_random_dtypes(dev, out_dtype, scale_dtype):
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(41)
+    rows, top, experts, o, k = 257, 3, 7, 256, 384
+    ids, active, counts, routes, x, xs, w, ws = _expert_case(rng, rows, top, experts, o, k, False,
+                                                             exact=False, mult=3)
+    sdt = getattr(torch, scale_dtype)
+    out = ops.expert_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev, sdt),
+                             _t(counts, dev), _t(routes, dev), r=rows, top=top,
+                             output_dtype=getattr(torch, out_dtype))
+    exp = omoe.expert_partial(x, xs, w, ws, counts, routes, top)
+    assert rel_fro(_np(out), exp) < (1e-4 if out_dtype == "float32" else 4e-3)
+
+
+def test_expert_partial_partitions_and_merge(dev):
+    from akas_amd import ops
+
+    rng = np.random.default_rng(43)
+    rows, top, experts, o, k = 33, 2, 4, 128, 512
+    ids, active, counts, routes, x, xs, w, ws = _expert_case(rng, rows, top, experts, o, k, False)
+    out = ops.expert_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev), _t(counts, dev),
+                             _t(routes, dev), r=rows, top=top, partitions=2)
+    exp = omoe.expert_partial(x, xs, w, ws, counts, routes, top, partitions=2)
+    np.testing.assert_array_equal(_np(out), exp)
+    merged = ops.expert_merge(out)
+    np.testing.assert_array_equal(_np(merged), omoe.expert_merge(exp))
+
+
+@pytest.mark.parametrize("routed", [False, True])
+def test_expert_partial_packed_input(dev, routed):
+    from akas_amd import ops
+
+    rng = np.random.default_rng(47)
+    rows, top, experts, o, k, maxm = 33, 3, 7, 256, 384, 64
+    ids, active, counts, routes, x, xs, w, ws = _expert_case(rng, rows, top, experts, o, k, routed)
+    te, tr = omoe.expert_tile_map(counts, rows, top, maxm)
+    px, pxs, offs = omoe.expert_pack(x, xs, counts, routes, top, experts, maxm, routed)
+    out = ops.expert_partial(_t(px, dev), _t(pxs, dev), _t(w, dev), _t(ws, dev), _t(counts, dev),
+                             _t(routes, dev), _t(te, dev), _t(tr, dev), _t(offs, dev), r=rows,
+                             top=top, packed_input=True, max_block_m=maxm)
+    exp = omoe.expert_partial(x, xs, w, ws, counts, routes, top, routed_input=routed)
+    np.testing.assert_array_equal(_np(out), exp)
+
+
+SWIGLU_CASES = [(1, 3, 7, 128, 256, "float32", "float32"),
+                (33, 3, 7, 256, 384, "float32", "float32"),
+                (33, 3, 7, 256, 384, "bfloat16", "bfloat16"),
+                (33, 3, 7, 256, 384, "float16", "float16"),
+                (257, 3, 7, 256, 384, "bfloat16", "bfloat16"),
+                (256, 4, 64, 256, 512, "bfloat16", "bfloat16"),
+                (2048, 4, 8, 256, 256, "float32", "bfloat16")]
+
+
+@pytest.mark.parametrize("rows,top,experts,o,k,pd,ad", SWIGLU_CASES)
+def test_fused_swiglu_matches_separate_chain_bitwise(dev, rows, top, experts, o, k, pd, ad):
+    """Fused gate/up/SwiGLU/re-quantization equals expert_partial x2 ->
+    swiglu_experts -> quantize bit for bit, on signed codes 32..80 and varying
+    scales (the reference's device equivalence recipe, seed 903,
+    tests/test_lfm_moe_native.py:295-347)."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(903)
+    ids, active = pattern_routes(rows, top, experts, 1)
+    counts, routes = omoe.quantized_routes(ids, active, experts)
+    x = random_codes(rng, (rows, k))
+    w = random_codes(rng, (experts, o, k))
+    w2 = random_codes(rng, (experts, o, k))
+    xs = rng.uniform(0.0625, 0.25, (rows, k // 128)).astype(np.float32)
+    ws = ofp8.bf16_round(rng.uniform(0.0625, 0.25, (experts, o // 128, k // 128)).astype(np.float32))
+    ws2 = ofp8.bf16_round(rng.uniform(0.0625, 0.25, (experts, o // 128, k // 128)).astype(np.float32))
+    P, A = getattr(torch, pd), getattr(torch, ad)
+    args = [_t(x, dev), _t(xs, dev)]
+    cnt, rts = _t(counts, dev), _t(routes, dev)
+    codes, scales = ops.fp8_expert_swiglu(*args, _t(w, dev), _t(ws, dev), _t(w2, dev), _t(ws2, dev),
+                                          cnt, rts, r=rows, top=top, product_dtype=P,
+                                          activation_dtype=A)
+    gate = ops.expert_partial(*args, _t(w, dev), _t(ws, dev), cnt, rts, r=rows, top=top,
+                              output_dtype=P)
+    up = ops.expert_partial(*args, _t(w2, dev), _t(ws2, dev), cnt, rts, r=rows, top=top,
+                            output_dtype=P)
+    act = ops.swiglu_experts(gate, up, output_dtype=A)
+    ecodes, escales = ops.quantize(act, top=top)
+    live = np.zeros((rows, top), bool)
+    for e in range(experts):
+        for route in routes[e, :counts[e]]:
+            live[route // top, route % top] = True
+    np.testing.assert_array_equal(_np(codes)[live], _np(ecodes)[live])
+    np.testing.assert_array_equal(_np(scales)[live], _np(escales)[live])
+    # and against the CPU oracle: dequantized activations within 1e-2
+    oc, osc, _ = omoe.fp8_expert_swiglu(x, xs, w, ws, w2, ws2, counts, routes, top, pd, ad)
+    got = ofp8.dequantize_activation(_np(codes), _np(scales))[live]
+    exp = ofp8.dequantize_activation(oc, osc)[live]
+    assert rel_fro(got, exp) < 1e-2
+
+
+@pytest.mark.parametrize("rows,top,experts,o,k,pd,ad", SWIGLU_CASES)
+def test_fused_swiglu_exact_products_midpoint_band(dev, rows, top, experts, o, k, pd, ad):
+    """Exact-product operands (codes {56,64} with sign, scales 0.125; seed 831):
+    codes equal the oracle except where the f32 activation interval straddles
+    an e4m3 midpoint; scales within 2e-6 (src/akas/ops/moe/validation.py:327-440)."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(831)
+    ids, active = pattern_routes(rows, top, experts, 1)
+    counts, routes = omoe.quantized_routes(ids, active, experts)
+    x, w, w2 = (exact_codes(rng, s) for s in ((rows, k), (experts, o, k), (experts, o, k)))
+    xs = np.full((rows, k // 128), 0.125, np.float32)
+    ws = np.full((experts, o // 128, k // 128), 0.125, np.float32)
+    codes, scales = ops.fp8_expert_swiglu(
+        _t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev), _t(w2, dev), _t(ws, dev),
+        _t(counts, dev), _t(routes, dev), r=rows, top=top, product_dtype=getattr(torch, pd),
+        activation_dtype=getattr(torch, ad))
+    oc, osc, norm = omoe.fp8_expert_swiglu(x, xs, w, ws, w2, ws, counts, routes, top, pd, ad)
+    live = np.zeros((rows, top), bool)
+    for e in range(experts):
+        for route in routes[e, :counts[e]]:
+            live[route // top, route % top] = True
+    ok = omoe.codes_within_midpoint_band(_np(codes), oc, norm)
+    assert ok[live].all()
+    np.testing.assert_allclose(_np(scales)[live], osc[live], rtol=2e-6, atol=1e-12)
+
+
+@pytest.mark.parametrize("pd,ad", [("float32", "float32"), ("bfloat16", "bfloat16")])
+def test_fused_swiglu_packed_in_out(dev, pd, ad):
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(1035)
+    rows, top, experts, o, k, maxm = 33, 3, 7, 256, 384, 64
+    ids, active = pattern_routes(rows, top, experts, 3)
+    counts, routes = omoe.quantized_routes(ids, active, experts)
+    x = random_codes(rng, (rows, k))
+    w = random_codes(rng, (experts, o, k))
+    w2 = random_codes(rng, (experts, o, k))
+    xs = rng.uniform(0.0625, 0.25, (rows, k // 128)).astype(np.float32)
+    ws = rng.uniform(0.0625, 0.25, (experts, o // 128, k // 128)).astype(np.float32)
+    ws2 = rng.uniform(0.0625, 0.25, (experts, o // 128, k // 128)).astype(np.float32)
+    te, tr = omoe.expert_tile_map(counts, rows, top, maxm)
+    px, pxs, offs = omoe.expert_pack(x, xs, counts, routes, top, experts, maxm)
+    P, A = getattr(torch, pd), getattr(torch, ad)
+    weights = [_t(w, dev), _t(ws, dev), _t(w2, dev), _t(ws2, dev)]
+    cnt, rts, tte, ttr = _t(counts, dev), _t(routes, dev), _t(te, dev), _t(tr, dev)
+    pc, psc = ops.fp8_expert_swiglu(_t(px, dev), _t(pxs, dev), *weights, cnt, rts, tte, ttr,
+                                    _t(offs, dev), r=rows, top=top, product_dtype=P,
+                                    activation_dtype=A, packed_input=True, packed_output=True,
+                                    max_block_m=maxm)
+    uc, usc = ops.fp8_expert_swiglu(_t(x, dev), _t(xs, dev), *weights, cnt, rts, r=rows, top=top,
+                                    product_dtype=P, activation_dtype=A)
+    pc, psc, uc, usc = _np(pc), _np(psc), _np(uc), _np(usc)
+    for e in range(experts):
+        for local, route in enumerate(routes[e, :counts[e]]):
+            row, rank = divmod(int(route), top)
+            np.testing.assert_array_equal(pc[offs[e] + local], uc[row, rank])
+            np.testing.assert_array_equal(psc[offs[e] + local], usc[row, rank])
+
+
+# ---------------------------------------------------------------------------
+# elementwise: swiglu, combine
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("parts", [1, 2])
+def test_swiglu_experts(dev, parts):
+    from akas_amd import ops
+
+    rng = np.random.default_rng(5)
+    shape = (9, 3, parts, 256) if parts > 1 else (9, 3, 256)
+    g = rng.normal(0, 3, shape).astype(np.float32)
+    u = rng.normal(0, 3, shape).astype(np.float32)
+    out = ops.swiglu_experts(_t(g, dev), _t(u, dev), round_inputs=True, round_dtype="bfloat16")
+    exp = omoe.swiglu_experts(g, u, round_inputs=True, round_dtype="bfloat16")
+    np.testing.assert_allclose(_np(out), exp, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("in_dtype", ["float32", "bfloat16"])
+def test_routed_combine(dev, in_dtype):
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(6)
+    rows, top, c = 33, 4, 2048
+    e = rng.normal(0, 1, (rows, top, c)).astype(np.float32)
+    if in_dtype == "bfloat16":
+        e = ofp8.bf16_round(e)
+    w = rng.uniform(0, 1, (rows, top)).astype(np.float32)
+    active = np.ones(rows, np.int32)
+    active[-1] = 0
+    out = ops.routed_combine(_t(e, dev, getattr(torch, in_dtype)), _t(w, dev), _t(active, dev))
+    np.testing.assert_allclose(_np(out), omoe.routed_combine(e, w, active), rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# the whole layer
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,packed,fused", [(256, False, True), (256, False, False),
+                                               (1000, True, True), (1, False, True)])
+def test_routed_moe_layer(dev, rows, packed, fused):
+    import torch
+    from akas_amd import moe
+
+    rng = np.random.default_rng(0)
+    H, F, E, top = 512, 256, 16, 4
+    x = bf16_normal(rng, (rows, H))
+    logits = rng.normal(0, 1, (rows, E)).astype(np.float32)
+    bank = {}
+    for name, shape in (("w1", (E, F, H)), ("w3", (E, F, H)), ("w2", (E, H, F))):
+        bank[name] = ofp8.quantize_weight_blocks(rng.normal(0, 0.05, shape).astype(np.float32))
+    wts = moe.ExpertWeights(*(_t(a, dev) for n in ("w1", "w3", "w2") for a in bank[n]))
+    out = moe.routed_moe(_t(x, dev, torch.bfloat16), _t(logits, dev), None, wts, top=top,
+                         packed=packed, fused_swiglu=fused)
+    exp, _, _ = omoe.moe_layer(x, logits, np.zeros(E, np.float32), *bank["w1"], *bank["w3"],
+                               *bank["w2"], top)
+    assert rel_fro(_np(out), exp) < 1e-2

@@ -1,0 +1,98 @@
+"""GPU parity: the FP8 activation quantizer is bit-exact against the oracle."""
+
+import numpy as np
+import pytest
+
+from oracle import fp8 as ofp8
+from golden_inputs import bf16_normal, stress_rows
+
+pytestmark = pytest.mark.gpu
+
+DT = {"float32": "float32", "float16": "float16", "bfloat16": "bfloat16"}
+
+
+def _to_device(x, dtype, dev):
+    import torch
+
+    t = torch.from_numpy(np.ascontiguousarray(x, np.float32))
+    return t.to(getattr(torch, dtype)).to(dev)
+
+
+def _run(x_np, dtype, dev, top=None):
+    import torch
+    from akas_amd import ops
+
+    x = _to_device(x_np, dtype, dev)
+    codes, scales = ops.quantize(x, top=top)
+    torch.cuda.synchronize()
+    # the oracle sees exactly the values the device read
+    xin = x.float().cpu().numpy()
+    ec, es = ofp8.quantize(xin)
+    return codes.cpu().numpy(), scales.cpu().numpy(), ec, es
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("top", [None, 4])
+def test_quantize_stress_and_random(dev, dtype, top):
+    rng = np.random.default_rng(17)
+    rows, k = 3, 384
+    x = stress_rows(k, rows * (top or 1), rng)
+    if top:
+        x = x.reshape(rows, top, k)
+    c, s, ec, es = _run(x, dtype, dev, top)
+    np.testing.assert_array_equal(c, ec)
+    np.testing.assert_array_equal(s, es)
+    # zero group: scale 1e-12/448, all codes +0
+    assert s.reshape(-1)[0] == np.float32(1e-12) / np.float32(448)
+    assert not c.reshape(-1, 128)[0].any()
+
+
+@pytest.mark.parametrize("shape", [(1, 2048), (16, 2048), (257, 1536), (8192, 2048)])
+def test_quantize_large_bit_exact(dev, shape):
+    rng = np.random.default_rng(0)
+    x = bf16_normal(rng, shape, outliers=0.01)
+    c, s, ec, es = _run(x, "bfloat16", dev)
+    np.testing.assert_array_equal(s, es)
+    np.testing.assert_array_equal(c, ec)
+
+
+def test_quantize_midpoints_and_subnormals(dev):
+    """Values placed exactly on and one ulp around e4m3 rounding midpoints,
+    after scaling, and in the e4m3 subnormal range."""
+    rng = np.random.default_rng(5)
+    codes = np.arange(0, 126, dtype=np.uint8)
+    lo, hi = ofp8.decode_e4m3(codes), ofp8.decode_e4m3(codes + 1)
+    mids = ((lo.astype(np.float64) + hi) / 2).astype(np.float32)
+    vals = np.concatenate([mids, np.nextafter(mids, 0), np.nextafter(mids, 1000),
+                           -mids, rng.uniform(-2 ** -6, 2 ** -6, 1000).astype(np.float32)])
+    vals = np.resize(vals, (64, 128 * 4)).astype(np.float32)
+    vals[:, ::128] = 448.0  # amax 448 -> scale exactly 1: values pass through unscaled
+    c, s, ec, es = _run(vals, "float32", dev)
+    np.testing.assert_array_equal(s, es)
+    np.testing.assert_array_equal(c, ec)
+
+
+def test_dequantize_round_trip(dev):
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(3)
+    x = bf16_normal(rng, (33, 1024))
+    c, s = ops.quantize(_to_device(x, "bfloat16", dev))
+    d = ops.dequantize_fp8(c, s).cpu().numpy()
+    exp = ofp8.dequantize_activation(c.cpu().numpy(), s.cpu().numpy())
+    np.testing.assert_array_equal(d, exp)
+
+
+@pytest.mark.parametrize("scale_dtype", ["float32", "bfloat16"])
+def test_weight_block_quantizer(dev, scale_dtype):
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(0)
+    w = rng.normal(0, 0.02, (2, 300, 512)).astype(np.float32)
+    codes, scales = ops.quantize_weight_blocks(torch.from_numpy(w).to(dev),
+                                               scale_dtype=getattr(torch, scale_dtype))
+    ec, es = ofp8.quantize_weight_blocks(w, scale_dtype)
+    np.testing.assert_array_equal(scales.float().cpu().numpy(), es)
+    np.testing.assert_array_equal(codes.cpu().numpy(), ec)
