@@ -61,6 +61,13 @@ def _out(t, name, shape, dtype, like):
     return _need(t, name, dtype, shape)
 
 
+def _out_dtype(out, out_dtype, default=torch.float32):
+    """Output dtype: explicit, else that of a caller-provided ``out``, else f32."""
+    if out_dtype is not None:
+        return _torch_dtype(out_dtype)
+    return out.dtype if out is not None else default
+
+
 _FLOATS = (torch.float32, torch.float16, torch.bfloat16)
 _SCALES = (torch.float32, torch.bfloat16)
 
@@ -90,12 +97,12 @@ def quantize(x, *, top=None, out=None, scales=None):
     return out, scales
 
 
-def dequantize_fp8(codes, scales, *, out=None, out_dtype=torch.float32):
+def dequantize_fp8(codes, scales, *, out=None, out_dtype=None):
     """``dequantize_fp8``: ``decode(codes) * scale`` per 128-group."""
     _need(codes, "codes", torch.uint8)
     k = codes.shape[-1]
     _need(scales, "scales", torch.float32, (*codes.shape[:-1], k // BLOCK))
-    out = _out(out, "out", tuple(codes.shape), _torch_dtype(out_dtype), codes)
+    out = _out(out, "out", tuple(codes.shape), _out_dtype(out, out_dtype), codes)
     check(_lib.load().akas_dequantize_fp8(_ptr(codes), _ptr(scales), _ptr(out), _dt(out.dtype),
                                           codes.numel() // k, k, _stream()), "dequantize_fp8")
     return out
@@ -140,7 +147,7 @@ def linear_workspace(r, k, o, device):
     return ws
 
 
-def fp8_linear(x, w, scales, *, out=None, out_dtype=torch.float32, workspace=None):
+def fp8_linear(x, w, scales, *, out=None, out_dtype=None, workspace=None):
     """``fp8_linear(r, k, o[, input_dtype]): x, w, scales -> out``.
 
     ``x`` f32/f16/bf16 ``[r, k]`` is quantized per 1x128 group, multiplied by
@@ -157,7 +164,7 @@ def fp8_linear(x, w, scales, *, out=None, out_dtype=torch.float32, workspace=Non
     if k % BLOCK or o % 16:
         raise ValueError("invalid FP8 projection geometry")
     _need(scales, "scales", _SCALES, ((o + BLOCK - 1) // BLOCK, k // BLOCK))
-    out = _out(out, "out", (r, o), _torch_dtype(out_dtype), x)
+    out = _out(out, "out", (r, o), _out_dtype(out, out_dtype), x)
     if workspace is None:
         workspace = linear_workspace(r, k, o, x.device)
     check(_lib.load().akas_fp8_linear(
@@ -167,7 +174,7 @@ def fp8_linear(x, w, scales, *, out=None, out_dtype=torch.float32, workspace=Non
 
 
 def projection_partial(x, activation_scales, w, scales, *, partitions=1, out=None,
-                       out_dtype=torch.float32):
+                       out_dtype=None):
     """``projection_partial(r, k, o, partitions)`` on prequantized codes.
 
     ``partitions == 1``: ``out [r, o]``; otherwise f32 ``[r, partitions, o]``.
@@ -182,7 +189,7 @@ def projection_partial(x, activation_scales, w, scales, *, partitions=1, out=Non
     _need(activation_scales, "activation_scales", torch.float32, (r, k // BLOCK))
     _need(scales, "scales", _SCALES, ((o + BLOCK - 1) // BLOCK, k // BLOCK))
     shape = (r, partitions, o) if partitions > 1 else (r, o)
-    dtype = torch.float32 if partitions > 1 else _torch_dtype(out_dtype)
+    dtype = torch.float32 if partitions > 1 else _out_dtype(out, out_dtype)
     out = _out(out, "out", shape, dtype, x)
     check(_lib.load().akas_projection_partial(
         _ptr(x), _ptr(activation_scales), _ptr(w), _ptr(scales), _dt(scales.dtype), _ptr(out),
@@ -190,18 +197,18 @@ def projection_partial(x, activation_scales, w, scales, *, partitions=1, out=Non
     return out
 
 
-def projection_merge(partial, *, out=None, out_dtype=torch.float32):
+def projection_merge(partial, *, out=None, out_dtype=None):
     """``projection_merge(r, o, partitions)``: serial f32 sum over partitions."""
     _need(partial, "partial", torch.float32)
     parts, o = partial.shape[-2:]
     rows = partial.numel() // (parts * o) if parts * o else 0
-    out = _out(out, "out", (*partial.shape[:-2], o), _torch_dtype(out_dtype), partial)
+    out = _out(out, "out", (*partial.shape[:-2], o), _out_dtype(out, out_dtype), partial)
     check(_lib.load().akas_projection_merge(_ptr(partial), _ptr(out), _dt(out.dtype), rows, o,
                                             parts, _stream()), "projection_merge")
     return out
 
 
-def expert_merge(partial, *, out=None, output_dtype=torch.float32):
+def expert_merge(partial, *, out=None, output_dtype=None):
     """``expert_merge(r, top, o, partitions)``: ``[r, top, parts, o] -> [r, top, o]``."""
     if partial.dim() != 4:
         raise ValueError("expert_merge expects [r, top, partitions, o]")
