@@ -14,6 +14,9 @@
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+// 16-byte staging word as a native vector (HIP's uint4 is a struct with a
+// union, which keeps arrays of it out of registers).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 namespace akas {
 
@@ -86,6 +89,32 @@ AKAS_DEV uint32_t e4m3_encode_scaled(float x, const GroupScale& g) {
   return e4m3_magnitude_code(q) | ((__float_as_uint(x) >> 24) & 128u);
 }
 
+// Signed quotient RN(x / s), clamped to 448 in magnitude.  |x| <= max|group|
+// bounds it by 448 * (1 + 2^-24) anyway; the clamp maps nothing to a new code
+// (all of (448, 464) encodes to 448).
+AKAS_DEV float scaled_quotient(float x, const GroupScale& g) {
+  const float q = __builtin_fminf(exact_quotient_magnitude(__builtin_fabsf(x), g), 448.0f);
+  return __builtin_copysignf(q, x);
+}
+
+// Hardware OCP-e4m3 conversion of two values into the low (HI=false) or high
+// (HI=true) 16 bits of `old`.  For |v| < 464 it is bit-identical to the
+// reference encoder (src/akas/quantization/_shared/e4m3.py:16-29), ties,
+// subnormals and signed zero included -- established by an exhaustive
+// comparison over every float32 pattern in that range on gfx950; above 464
+// it would produce NaN, which scaled_quotient() rules out.
+template <bool HI>
+AKAS_DEV uint32_t cvt_e4m3x2(float a, float b, uint32_t old) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)old, HI);
+}
+
+// Four scaled values -> four codes in one word (byte i = value i).
+AKAS_DEV uint32_t e4m3_encode4_scaled(float x0, float x1, float x2, float x3,
+                                      const GroupScale& g) {
+  const uint32_t w = cvt_e4m3x2<false>(scaled_quotient(x0, g), scaled_quotient(x1, g), 0u);
+  return cvt_e4m3x2<true>(scaled_quotient(x2, g), scaled_quotient(x3, g), w);
+}
+
 // ---------------------------------------------------------------------------
 // bf16 / f16 conversions (round to nearest even, finite inputs)
 // ---------------------------------------------------------------------------
@@ -139,6 +168,16 @@ AKAS_DEV void store_elem(void* p, int64_t i, float v, int dtype) {
 AKAS_DEV float load_scale(const void* p, int64_t i, int scale_dtype) {
   return scale_dtype == AKAS_DTYPE_F32 ? ((const float*)p)[i]
                                        : bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+
+// Compile-time-dtype form for hot loops: a runtime dtype branch around a
+// global load makes the compiler drain every outstanding load at the join.
+template <int SDT>
+AKAS_DEV float load_scale_t(const void* p, int64_t i) {
+  if constexpr (SDT == AKAS_DTYPE_F32)
+    return reinterpret_cast<const float*>(p)[i];
+  else
+    return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
 }
 
 // ---------------------------------------------------------------------------

@@ -30,8 +30,14 @@ AKAS_DEV void grouped_tile(int id, int tiles_m, int tiles_n, int G, int& tm, int
 
 // ---------------------------------------------------------------------------
 // LDS-tiled MFMA GEMM (prefill shapes and medium M)
+//
+// DEPTH k-blocks are in flight per workgroup in a register ring in front of
+// the two LDS stages: at k-block kb the ring holds kb+1 .. kb+DEPTH, so the
+// HBM latency of a load is covered by DEPTH k-block multiplies.  Decode-sized
+// launches (few tiles, 16 k-blocks) need DEPTH 3-4; prefill tiles fill the
+// GPU with enough workgroups that DEPTH 1 suffices.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, int WAVES_M, int WAVES_N, int OUT>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int DEPTH, int OUT, int SDT>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void dense_tiled_kernel(DenseArgs p) {
   constexpr int THREADS = 64 * WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
@@ -76,29 +82,63 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void dense_tiled_kernel(Den
 
   Acc<MT, NT> acc;
   acc.clear();
-  uint4 r[Plan::CA + Plan::CB];
-  float ras = 0.f;
-
-  plan.fetch(kb0, r);
-  ras = as_row[kb0];
-  plan.stash(lds, r);
-  if (tid < BM) lds_as[0][tid] = ras;
+  // Ring slot = (A chunks, B chunks, activation scale, weight scale) of one
+  // k-block.  Every global load, scales included, is issued DEPTH k-blocks
+  // before its use: loads complete in issue order, so a scale fetched after
+  // a prefetch would make the current multiply wait for that prefetch.
+  u32x4 ring_a[DEPTH][Plan::CA], ring_b[DEPTH][Plan::CB];
+  float ras[DEPTH], rws[DEPTH];
+  const int last = kb1 - 1;
+  // prologue: k-blocks kb0 .. kb0+DEPTH-1 in flight; stage 0 <- kb0
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    const int k = min(kb0 + d, last);
+    plan.fetch(k, ring_a[d], ring_b[d]);
+    ras[d] = as_row[k];
+    rws[d] = load_scale_t<SDT>(p.ws, ws_base + k);
+  }
+  plan.stash(lds, ring_a[0], ring_b[0]);
+  if (tid < BM) lds_as[0][tid] = ras[0];
+  float ws_cur = rws[0];
+  {
+    const int k = min(kb0 + DEPTH, last);
+    plan.fetch(k, ring_a[0], ring_b[0]);
+    ras[0] = as_row[k];
+    rws[0] = load_scale_t<SDT>(p.ws, ws_base + k);
+  }
   __syncthreads();
 
-  // The prefetch is unconditional (the last iteration re-reads its own block
-  // into the idle stage) so the staging registers never live in scratch.
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const int cur = (kb - kb0) & 1;
-    const int nxt = min(kb + 1, kb1 - 1);
-    plan.fetch(nxt, r);
-    ras = as_row[nxt];
-    const float ws = load_scale(p.ws, ws_base + kb, p.ws_dtype);
-    mma_stage<MT, NT>(acc, lds + cur * STAGE, lds + cur * STAGE + BM * 128, lds_as[cur], a_row0,
-                      b_row0, ws, lane);
-    plan.stash(lds + (cur ^ 1) * STAGE, r);
-    if (tid < BM) lds_as[cur ^ 1][tid] = ras;
-    __syncthreads();
+  // Ring slot of k-block k is (k - kb0) % DEPTH; the loop body is expanded
+  // DEPTH times with constant slot indices so the ring stays in registers.
+  // Ring traffic is unconditional: past the last k-block it re-reads that
+  // block into the idle stage, which is never consumed.
+#define AKAS_RING_STEP(J)                                                            \
+  if constexpr ((J) < DEPTH) {                                                       \
+    const int k = kb + (J);                                                          \
+    const int cur = (k - kb0) & 1;                                                   \
+    if (k < kb1)                                                                     \
+      mma_stage<MT, NT>(acc, lds + cur * STAGE, lds + cur * STAGE + BM * 128,        \
+                        lds_as[cur], a_row0, b_row0, ws_cur, lane);                  \
+    constexpr int ns = ((J) + 1) % DEPTH;                                            \
+    plan.stash(lds + (cur ^ 1) * STAGE, ring_a[ns], ring_b[ns]);                     \
+    if (tid < BM) lds_as[cur ^ 1][tid] = ras[ns];                                    \
+    ws_cur = rws[ns];                                                                \
+    const int kf = min(k + 1 + DEPTH, last);                                         \
+    plan.fetch(kf, ring_a[ns], ring_b[ns]);                                          \
+    ras[ns] = as_row[kf];                                                            \
+    rws[ns] = load_scale_t<SDT>(p.ws, ws_base + kf);                            \
+    __syncthreads();                                                                 \
   }
+  for (int kb = kb0; kb < kb1; kb += DEPTH) {
+    AKAS_RING_STEP(0)
+    AKAS_RING_STEP(1)
+    AKAS_RING_STEP(2)
+    AKAS_RING_STEP(3)
+    AKAS_RING_STEP(4)
+    AKAS_RING_STEP(5)
+  }
+#undef AKAS_RING_STEP
+  static_assert(DEPTH >= 1 && DEPTH <= 6, "prefetch depth 1..6");
 
   const int64_t obase = (int64_t)part * p.part_stride;
 #pragma unroll
@@ -119,7 +159,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void dense_tiled_kernel(Den
 // (weights stream once from HBM, activations hit L2), then a fixed-order
 // LDS reduction of the four partial tiles.
 // ---------------------------------------------------------------------------
-template <int MT, int OUT>
+template <int MT, int OUT, int SDT>
 __global__ __launch_bounds__(256) void dense_small_kernel(DenseArgs p) {
   constexpr int U = MT <= 2 ? 4 : 2;  // k-blocks in flight per wave
   __shared__ __attribute__((aligned(16))) float red[4][MT][64][4];
@@ -170,7 +210,7 @@ __global__ __launch_bounds__(256) void dense_small_kernel(DenseArgs p) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) sv[u][i][e] = srow[i][e] ? srow[i][e][k] : 0.f;
         }
-        wsv[u] = load_scale(p.ws, ws_base + k, p.ws_dtype);
+        wsv[u] = load_scale_t<SDT>(p.ws, ws_base + k);
       }
     }
 #pragma unroll
@@ -214,6 +254,123 @@ __global__ __launch_bounds__(256) void dense_small_kernel(DenseArgs p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Wide small-M MFMA GEMM (M <= 64): one workgroup of NTW x KS waves covers
+// 16*NTW columns and the partition's whole k range.  The activation slab
+// (codes and scales of all its rows) is staged in LDS once per workgroup,
+// every wave issues all of its weight loads up front (k-blocks strided by
+// KS), multiplies, and the KS partial tiles are summed in a fixed order.
+// Weights stream from HBM exactly once; activations are read from L2 once
+// per workgroup instead of once per wave.
+// ---------------------------------------------------------------------------
+constexpr int kWideBatch = 4;  // k-blocks of weights in flight per wave
+
+template <int MT, int NTW, int KS>
+constexpr size_t wide_lds_bytes(int kbp) {
+  const size_t stage = (size_t)kbp * 16 * MT * (128 + 4);
+  const size_t red = (size_t)KS * NTW * MT * 64 * 16;
+  return stage > red ? stage : red;
+}
+
+template <int MT, int NTW, int KS, int OUT, int SDT>
+__global__ __launch_bounds__(64 * NTW * KS) void dense_wide_kernel(DenseArgs p) {
+  constexpr int THREADS = 64 * NTW * KS;
+  constexpr int ROWS = 16 * MT;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int KB = p.K / kBlock;
+  const int part = blockIdx.y;
+  const int kb0 = part * p.kb_per_part, kbp = p.kb_per_part;
+  uint8_t* lds_a = smem;                                            // [kbp][ROWS][128]
+  float* lds_s = reinterpret_cast<float*>(smem + (size_t)kbp * ROWS * 128);  // [kbp][ROWS]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nt = wave % NTW, ks = wave / NTW;
+  const int n0 = blockIdx.x * (16 * NTW) + nt * 16;
+  const int g = lane >> 4, r16 = lane & 15;
+  const uint8_t* wrow = p.w + (int64_t)(n0 + r16) * p.K + g * 32;
+  const int64_t ws_base = (int64_t)(n0 / kBlock) * KB;
+
+  // 1. first batch of this wave's weight loads (local k-blocks ks, ks+KS, ...)
+  u32x4 wl[kWideBatch][2];
+  float wsv[kWideBatch];
+  auto issue = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < kWideBatch; ++j) {
+      const int lk = ks + KS * (b * kWideBatch + j);
+      if (lk < kbp) {
+        const int64_t ko = (int64_t)(kb0 + lk) * kBlock;
+        wl[j][0] = *reinterpret_cast<const u32x4*>(wrow + ko);
+        wl[j][1] = *reinterpret_cast<const u32x4*>(wrow + ko + 16);
+        wsv[j] = load_scale_t<SDT>(p.ws, ws_base + kb0 + lk);
+      }
+    }
+  };
+  issue(0);
+
+  // 2. stage the activation slab (rows past M are zero) and its scales
+  for (int c = tid; c < ROWS * kbp * 8; c += THREADS) {
+    const int row = c / (kbp * 8), rem = c % (kbp * 8), lk = rem >> 3, ch = rem & 7;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (row < p.M)
+      v = *reinterpret_cast<const u32x4*>(p.a + (int64_t)row * p.K + (int64_t)(kb0 + lk) * kBlock + ch * 16);
+    *reinterpret_cast<u32x4*>(lds_a + (size_t)lk * ROWS * 128 + lds_off(row, ch)) = v;
+  }
+  for (int c = tid; c < ROWS * kbp; c += THREADS) {
+    const int lk = c / ROWS, row = c % ROWS;
+    lds_s[c] = row < p.M ? p.as[(int64_t)row * KB + kb0 + lk] : 0.f;
+  }
+  __syncthreads();
+
+  // 3. multiply batch by batch
+  v4f acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int batches = (kbp + KS * kWideBatch - 1) / (KS * kWideBatch);
+  for (int b = 0; b < batches; ++b) {
+    if (b > 0) issue(b);
+#pragma unroll
+    for (int j = 0; j < kWideBatch; ++j) {
+      const int lk = ks + KS * (b * kWideBatch + j);
+      if (lk < kbp) {
+        v8i bf;
+        bf[0] = wl[j][0][0]; bf[1] = wl[j][0][1]; bf[2] = wl[j][0][2]; bf[3] = wl[j][0][3];
+        bf[4] = wl[j][1][0]; bf[5] = wl[j][1][1]; bf[6] = wl[j][1][2]; bf[7] = wl[j][1][3];
+        const uint8_t* at = lds_a + (size_t)lk * ROWS * 128;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const v8i af = lds_fragment(at, 16 * i, lane);
+          const float4 s4 = *reinterpret_cast<const float4*>(lds_s + lk * ROWS + 16 * i + 4 * g);
+          const v4f pr = mfma_e4m3(af, bf);
+          acc[i][0] = __builtin_fmaf(pr[0], s4.x * wsv[j], acc[i][0]);
+          acc[i][1] = __builtin_fmaf(pr[1], s4.y * wsv[j], acc[i][1]);
+          acc[i][2] = __builtin_fmaf(pr[2], s4.z * wsv[j], acc[i][2]);
+          acc[i][3] = __builtin_fmaf(pr[3], s4.w * wsv[j], acc[i][3]);
+        }
+      }
+    }
+  }
+
+  // 4. fixed-order sum of the KS partial tiles (LDS slab reused)
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+    *reinterpret_cast<float4*>(red + (((ks * NTW + nt) * MT + i) * 64 + lane) * 4) =
+        make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+  __syncthreads();
+  if (ks == 0) {
+    const int64_t obase = (int64_t)part * p.part_stride;
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = red[((nt * MT + i) * 64 + lane) * 4 + e];
+        for (int q = 1; q < KS; ++q) v += red[(((q * NTW + nt) * MT + i) * 64 + lane) * 4 + e];
+        const int row = 16 * i + 4 * g + e;
+        if (row < p.M) store_out<OUT>(p.out, obase + (int64_t)row * p.ldo + n0 + r16, v);
+      }
+  }
+}
+
 // Serial f32 sum over partitions (src/akas/ops/linear/cuda.py:1369-1402).
 __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ partial,
                                                     void* __restrict__ out, int out_dtype,
@@ -229,34 +386,66 @@ __global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ pa
   }
 }
 
-template <int BM, int BN, int WMW, int WNW, int OUT>
+template <int BM, int BN, int WMW, int WNW, int DEPTH, int OUT, int SDT>
 static void launch_tiled(const DenseArgs& a, int parts, hipStream_t s) {
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  dense_tiled_kernel<BM, BN, WMW, WNW, OUT><<<dim3(tiles, parts), 64 * WMW * WNW, 0, s>>>(a);
+  dense_tiled_kernel<BM, BN, WMW, WNW, DEPTH, OUT, SDT>
+      <<<dim3(tiles, parts), 64 * WMW * WNW, 0, s>>>(a);
 }
 
 // Kernel choice by shape: the direct-load small-M kernel up to 64 rows;
 // beyond that LDS-tiled 256x256 tiles when they fill the GPU, 128x128
 // otherwise.  Tiled kernels need N to be a multiple of their BN (B rows are
 // addressed affinely); other N fall back to 64-row slices of the small kernel.
-template <int OUT>
+template <int OUT, int SDT>
 static void launch_small(const DenseArgs& a, int parts, hipStream_t s) {
   if (a.M <= 16)
-    dense_small_kernel<1, OUT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
+    dense_small_kernel<1, OUT, SDT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
   else if (a.M <= 32)
-    dense_small_kernel<2, OUT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
+    dense_small_kernel<2, OUT, SDT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
   else
-    dense_small_kernel<4, OUT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
+    dense_small_kernel<4, OUT, SDT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
 }
 
-template <int OUT>
+template <int MT, int NTW, int KS, int OUT, int SDT>
+static bool launch_wide(const DenseArgs& a, int parts, hipStream_t s) {
+  const size_t lds = wide_lds_bytes<MT, NTW, KS>(a.kb_per_part);
+  if (lds > 160 * 1024 || a.N % (16 * NTW)) return false;
+  auto kern = dense_wide_kernel<MT, NTW, KS, OUT, SDT>;
+  static bool configured = false;  // attribute set once per instantiation
+  if (!configured) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    configured = true;
+  }
+  kern<<<dim3(a.N / (16 * NTW), parts), 64 * NTW * KS, lds, s>>>(a);
+  return true;
+}
+
+// Kernel choice by shape (measured on MI355X, K = 2048, N = 6144):
+//   M <= 64   wide kernel (activations staged once per workgroup in LDS)
+//   M <= 256  64x64 tiles, 2 k-blocks of prefetch
+//   larger    256x128 tiles when they fill the GPU, else 128x128
+// Tiled kernels need N to be a multiple of BN (affine B rows); shapes that
+// fit none of these fall back to 64-row slices of the direct small kernel.
+template <int OUT, int SDT>
 static void launch_dense_t(const DenseArgs& a, int parts, hipStream_t s) {
+  bool done = false;
+  if (a.M <= 16)
+    done = launch_wide<1, 2, 8, OUT, SDT>(a, parts, s);
+  else if (a.M <= 32)
+    done = launch_wide<2, 2, 8, OUT, SDT>(a, parts, s);
+  else if (a.M <= 64)
+    done = launch_wide<4, 2, 8, OUT, SDT>(a, parts, s);
+  if (done) return;
   if (a.M <= 64) {
-    launch_small<OUT>(a, parts, s);
+    launch_small<OUT, SDT>(a, parts, s);
+  } else if (a.M <= 256 && a.N % 64 == 0) {
+    launch_tiled<64, 64, 2, 2, 2, OUT, SDT>(a, parts, s);
   } else if (a.N % 128 == 0 && (int64_t)((a.M + 255) / 256) * (a.N / 128) >= 512) {
-    launch_tiled<256, 128, 4, 2, OUT>(a, parts, s);
+    launch_tiled<256, 128, 4, 2, 1, OUT, SDT>(a, parts, s);
   } else if (a.N % 128 == 0) {
-    launch_tiled<128, 128, 2, 2, OUT>(a, parts, s);
+    launch_tiled<128, 128, 2, 2, 1, OUT, SDT>(a, parts, s);
   } else {
     const int esz = OUT == AKAS_DTYPE_F32 ? 4 : 2;
     for (int m0 = 0; m0 < a.M; m0 += 64) {
@@ -265,16 +454,24 @@ static void launch_dense_t(const DenseArgs& a, int parts, hipStream_t s) {
       b.a = a.a + (int64_t)m0 * a.K;
       b.as = a.as + (int64_t)m0 * (a.K / kBlock);
       b.out = reinterpret_cast<char*>(a.out) + (int64_t)m0 * a.ldo * esz;
-      launch_small<OUT>(b, parts, s);
+      launch_small<OUT, SDT>(b, parts, s);
     }
   }
 }
 
+template <int OUT>
+static void launch_dense_o(const DenseArgs& a, int parts, hipStream_t s) {
+  if (a.ws_dtype == AKAS_DTYPE_F32)
+    launch_dense_t<OUT, AKAS_DTYPE_F32>(a, parts, s);
+  else
+    launch_dense_t<OUT, AKAS_DTYPE_BF16>(a, parts, s);
+}
+
 int launch_dense(const DenseArgs& a, int parts, hipStream_t s) {
   switch (a.out_dtype) {
-    case AKAS_DTYPE_F32: launch_dense_t<AKAS_DTYPE_F32>(a, parts, s); break;
-    case AKAS_DTYPE_BF16: launch_dense_t<AKAS_DTYPE_BF16>(a, parts, s); break;
-    default: launch_dense_t<AKAS_DTYPE_F16>(a, parts, s);
+    case AKAS_DTYPE_F32: launch_dense_o<AKAS_DTYPE_F32>(a, parts, s); break;
+    case AKAS_DTYPE_BF16: launch_dense_o<AKAS_DTYPE_BF16>(a, parts, s); break;
+    default: launch_dense_o<AKAS_DTYPE_F16>(a, parts, s);
   }
   return hipGetLastError() == hipSuccess ? AKAS_OK : AKAS_ERR_LAUNCH;
 }

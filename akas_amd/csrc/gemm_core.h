@@ -44,21 +44,24 @@ struct StagePlan {
   uint32_t b_step;        // bytes between this thread's successive B rows
   int dst0;               // LDS offset of this thread's first chunk
 
-  AKAS_DEV void fetch(int kb, uint4 (&r)[CA + CB]) const {
+  // Staging registers are kept in two small arrays (A chunks, B chunks):
+  // one 128-byte array of uint4 is past what the alloca promotion keeps in
+  // registers and would be placed in scratch.
+  AKAS_DEV void fetch(int kb, u32x4 (&ra)[CA], u32x4 (&rb)[CB]) const {
     const uint32_t ko = (uint32_t)kb * kBlock;
 #pragma unroll
-    for (int i = 0; i < CA; ++i) r[i] = *reinterpret_cast<const uint4*>(a_base + (a_off[i] + ko));
+    for (int i = 0; i < CA; ++i) ra[i] = *reinterpret_cast<const u32x4*>(a_base + (a_off[i] + ko));
 #pragma unroll
     for (int j = 0; j < CB; ++j)
-      r[CA + j] = *reinterpret_cast<const uint4*>(b_base + (b_off + j * b_step + ko));
+      rb[j] = *reinterpret_cast<const u32x4*>(b_base + (b_off + j * b_step + ko));
   }
-  AKAS_DEV void stash(uint8_t* stage, const uint4 (&r)[CA + CB]) const {
+  AKAS_DEV void stash(uint8_t* stage, const u32x4 (&ra)[CA], const u32x4 (&rb)[CB]) const {
 #pragma unroll
     for (int i = 0; i < CA; ++i)
-      *reinterpret_cast<uint4*>(stage + dst0 + i * RSTEP * 128) = r[i];
+      *reinterpret_cast<u32x4*>(stage + dst0 + i * RSTEP * 128) = ra[i];
 #pragma unroll
     for (int j = 0; j < CB; ++j)
-      *reinterpret_cast<uint4*>(stage + BM * 128 + dst0 + j * RSTEP * 128) = r[CA + j];
+      *reinterpret_cast<u32x4*>(stage + BM * 128 + dst0 + j * RSTEP * 128) = rb[j];
   }
 };
 
@@ -77,11 +80,11 @@ struct Acc {
 // Load one MFMA operand fragment (16 rows x 128 k) for this lane from LDS.
 AKAS_DEV v8i lds_fragment(const uint8_t* tile, int row0, int lane) {
   const int row = row0 + (lane & 15), g = lane >> 4;
-  uint4 lo = *reinterpret_cast<const uint4*>(tile + lds_off(row, 2 * g));
-  uint4 hi = *reinterpret_cast<const uint4*>(tile + lds_off(row, 2 * g + 1));
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(tile + lds_off(row, 2 * g));
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(tile + lds_off(row, 2 * g + 1));
   v8i f;
-  f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
-  f[4] = hi.x; f[5] = hi.y; f[6] = hi.z; f[7] = hi.w;
+  f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
+  f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
   return f;
 }
 

@@ -77,7 +77,7 @@ AKAS_DEV int source_row(const ExpertArgs& p, int e, int idx) {
 
 // MODE 0: expert_partial (scatter f32/f16/bf16 to out[route][part][col]).
 // MODE 1: fp8_expert_swiglu (B tile = 16-row gate/up tiles interleaved).
-template <int BM, int BN, int WAVES_M, int WAVES_N, int MODE, int OUT>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int MODE, int OUT, int SDT>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(ExpertArgs p) {
   constexpr int THREADS = 64 * WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
@@ -150,25 +150,39 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
 
   Acc<MT, NT> acc;
   acc.clear();
-  uint4 r[Plan::CA + Plan::CB];
-  float ras;
-  plan.fetch(kb0, r);
+  // Every global load (data and both scales) is issued one k-block before its
+  // use: loads complete in issue order, so a scale fetched after the
+  // prefetch would make the current multiply wait for that prefetch.
+  u32x4 ra[Plan::CA], rb[Plan::CB];
+  float ras, rws0, rws1 = 0.f;
+  plan.fetch(kb0, ra, rb);
   ras = as_row[kb0];
-  plan.stash(lds, r);
+  float ws0 = load_scale_t<SDT>(p.ws, ws_base + kb0);
+  float ws1 = PAIRED ? load_scale_t<SDT>(p.ws2, ws_base + kb0) : 0.f;
+  plan.stash(lds, ra, rb);
   if (tid < BM) lds_as[0][tid] = ras;
+  {
+    const int nxt = min(kb0 + 1, kb1 - 1);
+    plan.fetch(nxt, ra, rb);
+    ras = as_row[nxt];
+    rws0 = load_scale_t<SDT>(p.ws, ws_base + nxt);
+    if constexpr (PAIRED) rws1 = load_scale_t<SDT>(p.ws2, ws_base + nxt);
+  }
   __syncthreads();
 
   for (int kb = kb0; kb < kb1; ++kb) {
     const int cur = (kb - kb0) & 1;
-    const int nxt = min(kb + 1, kb1 - 1);
-    plan.fetch(nxt, r);
-    ras = as_row[nxt];
-    const float ws0 = load_scale(p.ws, ws_base + kb, p.ws_dtype);
-    const float ws1 = PAIRED ? load_scale(p.ws2, ws_base + kb, p.ws_dtype) : 0.f;
     mma_stage<MT, NT, PAIRED>(acc, lds + cur * STAGE, lds + cur * STAGE + BM * 128, lds_as[cur],
                               a_row0, b_row0, ws0, lane, ws1);
-    plan.stash(lds + (cur ^ 1) * STAGE, r);
+    plan.stash(lds + (cur ^ 1) * STAGE, ra, rb);
     if (tid < BM) lds_as[cur ^ 1][tid] = ras;
+    ws0 = rws0;
+    ws1 = rws1;
+    const int nxt = min(kb + 2, kb1 - 1);
+    plan.fetch(nxt, ra, rb);
+    ras = as_row[nxt];
+    rws0 = load_scale_t<SDT>(p.ws, ws_base + nxt);
+    if constexpr (PAIRED) rws1 = load_scale_t<SDT>(p.ws2, ws_base + nxt);
     __syncthreads();
   }
 
@@ -254,7 +268,10 @@ static void launch_expert(ExpertArgs a, hipStream_t s) {
   a.max_tiles = (int)capacity_tiles(a.r, a.top, a.E, BM);
   a.tiles_n = MODE == 1 ? a.N / (BN / 2) : a.N / BN;
   dim3 grid((unsigned)(a.max_tiles * a.tiles_n), (unsigned)a.parts);
-  expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT><<<grid, 64 * WMW * WNW, 0, s>>>(a);
+  if (a.ws_dtype == AKAS_DTYPE_F32)
+    expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_F32><<<grid, 64 * WMW * WNW, 0, s>>>(a);
+  else
+    expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_BF16><<<grid, 64 * WMW * WNW, 0, s>>>(a);
 }
 
 // Row tile by the mean rows per expert: 32-row tiles for decode-like batches,

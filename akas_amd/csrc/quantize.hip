@@ -54,11 +54,8 @@ __global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ 
 #pragma unroll
     for (int o = 8; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o, 16));
     const GroupScale gs = make_group_scale(m);
-    uint32_t lo = 0, hi = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lo |= e4m3_encode_scaled(v[i], gs) << (8 * i);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hi |= e4m3_encode_scaled(v[4 + i], gs) << (8 * i);
+    const uint32_t lo = e4m3_encode4_scaled(v[0], v[1], v[2], v[3], gs);
+    const uint32_t hi = e4m3_encode4_scaled(v[4], v[5], v[6], v[7], gs);
     *reinterpret_cast<uint2*>(out + base) = make_uint2(lo, hi);
     if (lane16 == 0) scales[g] = gs.s;
   }

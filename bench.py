@@ -106,6 +106,23 @@ def time_kernel(torch, fn, reps, hold_ms=None):
     return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / reps  # ms
 
 
+def time_kernel_graph(torch, fn, n, replays=5):
+    """Average GPU duration per launch of ``fn(i)``, from a HIP graph of ``n``
+    back-to-back launches timed with one event pair per replay (no per-launch
+    event packets, no host dispatch gaps)."""
+    g = graph_of(torch, fn, n)
+    g.replay()
+    a = [torch.cuda.Event(enable_timing=True) for _ in range(replays)]
+    b = [torch.cuda.Event(enable_timing=True) for _ in range(replays)]
+    torch.cuda.synchronize()
+    for i in range(replays):
+        a[i].record()
+        g.replay()
+        b[i].record()
+    torch.cuda.synchronize()
+    return min(x.elapsed_time(y) for x, y in zip(a, b)) / n  # ms, best replay
+
+
 def graph_of(torch, fn, n):
     """HIP graph of ``fn(0) .. fn(n-1)`` on a side stream (warmed up first)."""
     s = torch.cuda.Stream()
@@ -155,10 +172,9 @@ def decode_sweep(torch, dev, steps, warmup):
     per_m = []
     for m in DECODE_M:
         q, qs = ops.quantize(xs[m])
-        reps = 40
-        ms = time_kernel(torch, lambda i: ops.projection_partial(
+        ms = time_kernel_graph(torch, lambda i: ops.projection_partial(
             q, qs, codes[i % copies], scales[i % copies], out=outs[m],
-            out_dtype=torch.bfloat16), reps)
+            out_dtype=torch.bfloat16), copies)
         b = gemm_kernel_bytes(m, K_DEC, N_DEC)
         per_m.append(dict(M=m, kernel_us=round(ms * 1e3, 3), bytes=b,
                           gbs=round(b / (ms * 1e-3) / 1e9, 1),
