@@ -25,6 +25,9 @@ FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
+    # Only the C ABI (declared with default visibility in include/akas_fp8.h)
+    # is exported; kernels and C++ helpers stay internal to the library.
+    "-fvisibility=hidden",
     # No packed FP32 instructions anywhere in this library.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # MFMA results in VGPRs: the per-block scale FMA reads them directly.
@@ -57,7 +60,8 @@ def build(verbose=False, jobs=None):
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         objs = list(pool.map(_compile, srcs))
     tmp = LIBRARY + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
+    # -Bsymbolic-functions: calls inside the library bind to its own definitions.
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-Bsymbolic-functions", *objs, "-o", tmp]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")

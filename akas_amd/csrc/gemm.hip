@@ -1,6 +1,7 @@
 // Dense block-scaled FP8 linear for gfx950: small-M (decode) and LDS-tiled
 // (prefill) MFMA kernels, split-K partials and the partition merge.
 #include "gemm_core.h"
+#include "gemm_dma.h"
 
 namespace akas {
 
@@ -151,6 +152,55 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void dense_tiled_kernel(Den
         const int col = wcol + 16 * j + (lane & 15);
         if (row < p.M && col < p.N) store_out<OUT>(p.out, obase + (int64_t)row * p.ldo + col, acc.t[i][j][e]);
       }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill GEMM: 256x256 tiles streamed into LDS by the gfx950 copy engine
+// (tile engine in gemm_dma.h).  N must be a multiple of 128 so that each
+// wave's 128 output columns are either all inside the matrix or all outside;
+// rows and columns past the ends are clamped on load and never stored.
+// ---------------------------------------------------------------------------
+template <int OUT, int SDT>
+__global__ __launch_bounds__(dma::THREADS) void dense_dma_kernel(DenseArgs p) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tiles_m = (p.M + dma::BM - 1) / dma::BM, tiles_n = (p.N + dma::BN - 1) / dma::BN;
+  const int id = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+  int tm, tn;
+  grouped_tile(id, tiles_m, tiles_n, 8, tm, tn);
+  const int m0 = tm * dma::BM, n0 = tn * dma::BN;
+  const int KB = p.K / kBlock;
+  const int part = blockIdx.y;
+  const int kb0 = part * p.kb_per_part, kb1 = kb0 + p.kb_per_part;
+
+  dma::AffinePlan plan;
+  const bool copies_a = wave < 4;
+  plan.src = copies_a ? p.a : p.w;
+  plan.blk0 = wave * 8;
+  {
+    const int row = dma::piece_row(wave, 0, lane);
+    plan.row0 = (uint32_t)((copies_a ? m0 : n0) + row);
+    plan.lim = (uint32_t)((copies_a ? p.M : p.N) - 1);
+    plan.ld = (uint32_t)p.K;
+    plan.chunk = (uint32_t)dma::piece_chunk(row, lane);
+  }
+  plan.as = p.as;
+  plan.soff = (uint32_t)min(m0 + (wave & 3) * 64 + lane, p.M - 1) * (uint32_t)KB;
+  plan.scales = copies_a;
+
+  const int a_row0 = (wave & 3) * 64, b_row0 = (wave >> 2) * 128;
+  const int col0 = n0 + b_row0;
+  const int64_t ws_base = (int64_t)min(col0 / kBlock, (p.N - 1) / kBlock) * KB;
+  dma::Acc acc;
+  acc.clear();
+  dma::run<false>(plan, acc, a_row0, b_row0, kb0, kb1, lane, [&](int kb) {
+    const float w = load_scale_t<SDT>(p.ws, ws_base + kb);
+    return float2{w, w};
+  });
+  const int64_t obase = (int64_t)part * p.part_stride + col0;
+  dma::store_tile<OUT>(
+      acc, p.out, wave, lane, [&](int r) { return m0 + a_row0 + r < p.M && col0 < p.N; },
+      [&](int r) { return obase + (int64_t)(m0 + a_row0 + r) * p.ldo; });
 }
 
 // ---------------------------------------------------------------------------
@@ -393,9 +443,25 @@ static void launch_tiled(const DenseArgs& a, int parts, hipStream_t s) {
       <<<dim3(tiles, parts), 64 * WMW * WNW, 0, s>>>(a);
 }
 
+// The DMA-fed 256x256 kernel takes over once its tiles cover the GPU at
+// least about once (fewer, larger tiles idle too many CUs) and the output
+// rows are 16-byte aligned for its vector stores.
+static bool dma_fits(const DenseArgs& a, int parts) {
+  const int esz = a.out_dtype == AKAS_DTYPE_F32 ? 4 : 2;
+  const int64_t tiles = (int64_t)((a.M + dma::BM - 1) / dma::BM) * ((a.N + dma::BN - 1) / dma::BN);
+  return a.N % 128 == 0 && tiles * parts >= 240 && (a.ldo * esz) % 16 == 0 &&
+         (a.part_stride * esz) % 16 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0;
+}
+
+template <int OUT, int SDT>
+static void launch_dma(const DenseArgs& a, int parts, hipStream_t s) {
+  const int tiles = ((a.M + dma::BM - 1) / dma::BM) * ((a.N + dma::BN - 1) / dma::BN);
+  dense_dma_kernel<OUT, SDT><<<dim3(tiles, parts), dma::THREADS, 0, s>>>(a);
+}
+
 // Kernel choice by shape: the direct-load small-M kernel up to 64 rows;
-// beyond that LDS-tiled 256x256 tiles when they fill the GPU, 128x128
-// otherwise.  Tiled kernels need N to be a multiple of their BN (B rows are
+// beyond that the DMA-fed 256x256 kernel when its tiles fill the GPU, else
+// LDS-tiled 256x128 / 128x128 tiles.  Tiled kernels need N to be a multiple of their BN (B rows are
 // addressed affinely); other N fall back to 64-row slices of the small kernel.
 template <int OUT, int SDT>
 static void launch_small(const DenseArgs& a, int parts, hipStream_t s) {
@@ -440,6 +506,8 @@ static void launch_dense_t(const DenseArgs& a, int parts, hipStream_t s) {
   if (done) return;
   if (a.M <= 64) {
     launch_small<OUT, SDT>(a, parts, s);
+  } else if (a.M > 256 && dma_fits(a, parts)) {
+    launch_dma<OUT, SDT>(a, parts, s);
   } else if (a.M <= 256 && a.N % 64 == 0) {
     launch_tiled<64, 64, 2, 2, 2, OUT, SDT>(a, parts, s);
   } else if (a.N % 128 == 0 && (int64_t)((a.M + 255) / 256) * (a.N / 128) >= 512) {

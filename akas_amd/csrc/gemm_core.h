@@ -11,15 +11,20 @@
 //
 // Workgroup tile BM x BN x 128, two LDS stages, global->register->LDS
 // prefetch of the next k-block while the current one is multiplied.  LDS rows
-// are 128 bytes with the 16-byte chunk index XOR-swizzled by (row >> 1) & 7 so
-// that the 16 rows read by one ds_read_b128 phase hit distinct banks.
+// are 128 bytes with the 16-byte chunk index XOR-swizzled by
+// (row & 7) ^ ((row >> 3) & 1): the 16 rows x 16 bytes that one quarter-wave
+// of a fragment's ds_read_b128 reads then fall on 16 distinct 16-byte bank
+// groups of the 256-byte-wide LDS (measured conflict-free with
+// SQ_LDS_BANK_CONFLICT; (row >> 1) & 7 and row & 7 both conflict 2-way).  The
+// swizzle depends on row % 16 only, so fragment addresses of tiles 16 rows
+// apart differ by a constant and fold into the instruction offset.
 #pragma once
 
 #include "common.h"
 
 namespace akas {
 
-AKAS_DEV int lds_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
+AKAS_DEV int lds_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row & 7) ^ ((row >> 3) & 1))) << 4); }
 
 // Staging plan: every thread moves CA chunks of the A tile and CB chunks of
 // the B tile per k-block.  Thread t owns chunk column (t % 8) of rows

@@ -1,0 +1,245 @@
+// 256x256 FP8 tile engine fed by direct global->LDS DMA (gfx950
+// global_load_lds_dwordx4), shared by the dense and the grouped expert GEMMs.
+//
+// C[m, n] = sum_kb ( A_kb[m, :] . B_kb[n, :] ) * as[m, kb] * ws[n / 128, kb]
+//
+// Workgroup: 8 waves (512 threads), tile 256 (A rows) x 256 (B rows) x 128.
+// Wave w multiplies A rows 64*(w%4) .. +63 against B rows 128*(w/4) .. +127,
+// so its B rows sit in one 128-row weight-scale block and the weight scale
+// of a k-block is one number per wave.
+//
+// LDS: two stages, each A tile (32 KB) then B tile (32 KB), 128-byte rows of
+// 16-byte chunks; chunk c of row r sits at slot c ^ swizzle(r) with
+// swizzle(r) = (r & 7) ^ ((r >> 3) & 1), which puts the 16 rows x 16 bytes read by
+// one quarter-wave of ds_read_b128 on 16 distinct 16-byte bank groups of the
+// 256-byte-wide LDS.  Each stage is its own __shared__ array and is selected
+// at compile time, so the compiler can tell that reads of one stage never
+// alias the DMA writes into the other one and does not wait for them.
+//
+// DMA: one global_load_lds_dwordx4 moves 64 lanes x 16 bytes into 1 KB of
+// LDS at M0 + 16 * lane, i.e. 8 consecutive 128-byte tile rows.  The lane
+// that lands in slot (lane & 7) of row r therefore fetches logical chunk
+// (lane & 7) ^ swizzle(r) of that row.  Each wave moves 8 KB (one quarter of
+// A for waves 0-3, of B for waves 4-7) per k-block, one piece per n-tile of
+// the multiply, so the copy engine runs while the MFMAs of the current stage
+// are issued; waves 0-3 also copy the 256 activation scales of the k-block.
+//
+// MFMA operands are swapped (weight fragment first), so lane l of a 16x16
+// product holds output row m = l % 16 and the four consecutive output columns
+// n = 4 * (l / 16) + e: the per-row activation scale is one value per lane
+// and the epilogue writes 4 adjacent columns per lane.
+#pragma once
+
+#include "common.h"
+
+namespace akas {
+namespace dma {
+
+constexpr int BM = 256, BN = 256, THREADS = 512;
+constexpr int STAGE = (BM + BN) * 128;
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+static __shared__ __attribute__((aligned(1024))) uint8_t stage0[STAGE];
+static __shared__ __attribute__((aligned(1024))) uint8_t stage1[STAGE];
+static __shared__ __attribute__((aligned(16))) float scales0[BM];
+static __shared__ __attribute__((aligned(16))) float scales1[BM];
+
+template <int S> AKAS_DEV uint8_t* stage_base() { return S ? stage1 : stage0; }
+template <int S> AKAS_DEV float* stage_scales() { return S ? scales1 : scales0; }
+
+AKAS_DEV int swizzle(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+AKAS_DEV int tile_off(int row, int chunk) { return row * 128 + ((chunk ^ swizzle(row)) << 4); }
+
+AKAS_DEV v8i fragment(const uint8_t* tile, int row0, int lane) {
+  const int row = row0 + (lane & 15), g = lane >> 4;
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(tile + tile_off(row, 2 * g));
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(tile + tile_off(row, 2 * g + 1));
+  v8i f;
+  f[0] = lo[0]; f[1] = lo[1]; f[2] = lo[2]; f[3] = lo[3];
+  f[4] = hi[0]; f[5] = hi[1]; f[6] = hi[2]; f[7] = hi[3];
+  return f;
+}
+
+// Tile row (0..255) of this lane in DMA piece i of a wave's quarter tile.
+AKAS_DEV int piece_row(int wave, int i, int lane) { return ((wave & 3) * 8 + i) * 8 + (lane >> 3); }
+// Byte offset within a source row of the chunk this lane fetches for tile row `row`.
+AKAS_DEV int piece_chunk(int row, int lane) { return ((lane & 7) ^ swizzle(row)) << 4; }
+
+// Per-wave copy plans.  offset(i) is the byte offset (k-block 0), relative
+// to src, of the 16 bytes this lane copies for piece i; rows past an
+// operand's end are clamped to a valid row (their products are never stored).
+//
+// AffinePlan: the wave's source rows are row0 + 8*i (+ lane/8 folded into
+// row0), clamped to lim -- contiguous operands.  The tile row of piece i is
+// 8*i below that of piece 0, whose bit 3 is clear, so its swizzle differs
+// from piece 0's in bit 0 exactly when i is odd: the chunk of piece i is
+// chunk ^ ((i & 1) << 4).
+struct AffinePlan {
+  const uint8_t* src;   // A codes for waves 0-3, B codes for waves 4-7
+  uint32_t row0;        // this lane's source row for piece 0
+  uint32_t lim;         // last valid source row
+  uint32_t ld;          // source row stride in bytes
+  uint32_t chunk;       // byte offset of this lane's chunk within a row (piece 0)
+  int blk0;             // first 1 KB LDS block of this wave within a stage
+  const float* as;      // activation scales (waves 0-3)
+  uint32_t soff;        // this lane's activation-scale offset (row * KB)
+  bool scales;          // wave copies activation scales
+  AKAS_DEV uint32_t offset(int i) const { return min(row0 + 8u * i, lim) * ld + (chunk ^ ((i & 1) << 4)); }
+};
+
+// GatherPlan: one arbitrary source offset per piece (rows gathered through
+// a route table).
+struct GatherPlan {
+  const uint8_t* src;
+  uint32_t off[8];
+  int blk0;
+  const float* as;
+  uint32_t soff;
+  bool scales;
+  AKAS_DEV uint32_t offset(int i) const { return off[i]; }
+};
+
+template <int S, class Plan>
+AKAS_DEV void copy_piece(const Plan& p, int i, uint32_t ko) {
+  __builtin_amdgcn_global_load_lds((const void*)(p.src + (p.offset(i) + ko)),
+                                   (lds_void*)(stage_base<S>() + (p.blk0 + i) * 1024), 16, 0, 0);
+}
+template <int S, class Plan>
+AKAS_DEV void copy_scales(const Plan& p, int kb) {
+  if (p.scales)
+    __builtin_amdgcn_global_load_lds((const void*)(p.as + (p.soff + kb)),
+                                     (lds_void*)(stage_scales<S>() + (p.blk0 >> 3) * 64), 4, 0, 0);
+}
+template <int S, class Plan>
+AKAS_DEV void copy_stage(const Plan& p, int kb) {
+  const uint32_t ko = (uint32_t)kb * 128;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) copy_piece<S>(p, i, ko);
+  copy_scales<S>(p, kb);
+}
+
+struct Acc {
+  v4f t[4][8];  // [m-tile][n-tile], lane: row l%16, columns 4*(l/16) .. +3
+  AKAS_DEV void clear() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+};
+
+// Multiply stage S into acc and stream k-block kb_next into stage 1-S.
+//   PAIRED: odd n-tiles use weight scale ws1 (gate/up tiles interleaved
+//   16 rows at a time), even n-tiles ws0.
+// Each n-tile's four products are folded right after their MFMAs: the fold
+// waits for the MFMA results, and the other wave on the SIMD issues its
+// MFMAs meanwhile (keeping the previous products in flight instead costs 16
+// registers and measured no faster).
+template <int S, bool PAIRED, class Plan>
+AKAS_DEV void multiply(const Plan& p, Acc& acc, int a_row0, int b_row0, float ws0, float ws1,
+                       int lane, int kb_next) {
+  const uint8_t* at = stage_base<S>();
+  const uint8_t* bt = at + BM * 128;
+  const uint32_t ko = (uint32_t)kb_next * 128;
+  v8i af[4];
+  float c0[4], c1[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    af[i] = fragment(at, a_row0 + 16 * i, lane);
+    const float s = stage_scales<S>()[a_row0 + 16 * i + (lane & 15)];
+    c0[i] = s * ws0;
+    c1[i] = PAIRED ? s * ws1 : c0[i];
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    copy_piece<1 - S>(p, j, ko);
+    if (j == 0) copy_scales<1 - S>(p, kb_next);
+    const v8i bf = fragment(bt, b_row0 + 16 * j, lane);
+    v4f cur[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cur[i] = mfma_e4m3(bf, af[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float c = (j & 1) ? c1[i] : c0[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc.t[i][j][e] = __builtin_fmaf(cur[i][e], c, acc.t[i][j][e]);
+    }
+  }
+}
+
+// Main loop over k-blocks [kb0, kb1).  ws(kb) returns (ws0, ws1) of a k-block
+// as a float2.  Every stage refills the other one with k-block
+// min(kb + 1, kb1 - 1): the refetch of the last block lands in a stage that
+// is never read again, and the closing barrier waits for it.
+template <bool PAIRED, class Plan, class WS>
+AKAS_DEV void run(const Plan& p, Acc& acc, int a_row0, int b_row0, int kb0, int kb1, int lane, WS ws) {
+  copy_stage<0>(p, kb0);
+  float2 wcur = ws(kb0);
+  __syncthreads();
+  const int last = kb1 - 1;
+  for (int kb = kb0; kb < kb1; kb += 2) {
+    float2 wnext = ws(min(kb + 1, last));
+    multiply<0, PAIRED>(p, acc, a_row0, b_row0, wcur.x, wcur.y, lane, min(kb + 1, last));
+    __syncthreads();
+    if (kb + 1 < kb1) {
+      wcur = wnext;
+      wnext = ws(min(kb + 2, last));
+      multiply<1, PAIRED>(p, acc, a_row0, b_row0, wcur.x, wcur.y, lane, min(kb + 2, last));
+      __syncthreads();
+      wcur = wnext;
+    }
+  }
+}
+
+AKAS_DEV uint32_t pack2(float lo, float hi, int dt) {
+  return dt == AKAS_DTYPE_BF16 ? f32x2_to_bf16x2(lo, hi) : (f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16));
+}
+
+// Write the wave's 64x128 tile.  16-bit outputs go through a per-wave 16 KB
+// LDS region (256-byte rows, 16-byte chunks XOR row) so that global stores
+// are full 16-byte lanes along rows; f32 outputs store 4 columns per lane
+// directly.  row_ok(r) / out_row(r) map a wave-local row to validity and to
+// the output element offset of its first column (columns are contiguous).
+// Must follow the main loop's closing barrier.
+template <int OUT, class RowOk, class OutRow>
+AKAS_DEV void store_tile(const Acc& acc, void* out, int wave, int lane, RowOk row_ok, OutRow out_row) {
+  if constexpr (OUT == AKAS_DTYPE_F32) {
+    float* o = reinterpret_cast<float*>(out);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * i + (lane & 15);
+      if (!row_ok(r)) continue;
+      const int64_t base = out_row(r);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int col = 16 * j + 4 * (lane >> 4);
+        *reinterpret_cast<float4*>(o + base + col) = float4{acc.t[i][j][0], acc.t[i][j][1], acc.t[i][j][2], acc.t[i][j][3]};
+      }
+    }
+  } else {
+    uint8_t* region = (wave < 4 ? stage0 : stage1) + (wave & 3) * 16384;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int r = 16 * i + (lane & 15);
+        const int col = 16 * j + 4 * (lane >> 4);
+        uint2 v;
+        v.x = pack2(acc.t[i][j][0], acc.t[i][j][1], OUT);
+        v.y = pack2(acc.t[i][j][2], acc.t[i][j][3], OUT);
+        *reinterpret_cast<uint2*>(region + r * 256 + (((col >> 3) ^ (r & 15)) << 4) + (col & 7) * 2) = v;
+      }
+    __syncthreads();
+    uint16_t* o = reinterpret_cast<uint16_t*>(out);
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      const int r = it * 4 + (lane >> 4), ch = lane & 15;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(region + r * 256 + ((ch ^ (r & 15)) << 4));
+      if (row_ok(r)) *reinterpret_cast<u32x4*>(o + out_row(r) + ch * 8) = v;
+    }
+  }
+}
+
+}  // namespace dma
+}  // namespace akas

@@ -36,6 +36,12 @@
 extern "C" {
 #endif
 
+/* The library is built with hidden visibility; only these entry points are
+   exported. */
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
 /* element dtype codes */
 #define AKAS_DTYPE_F32 0
 #define AKAS_DTYPE_F16 1
@@ -267,6 +273,10 @@ int akas_swiglu_experts(const void* g, const void* u, int input_dtype, void* out
 int akas_routed_combine(const void* experts, int input_dtype, const float* weights,
                         const int32_t* active, float* out, int64_t r, int top, int64_t c,
                         void* stream);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
 
 #ifdef __cplusplus
 }
