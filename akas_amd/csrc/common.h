@@ -146,7 +146,12 @@ AKAS_DEV float f16_bits_to_f32(uint32_t h) {
   return (float)x;
 }
 
+// The empty asm pins v as a finished float32: without it the compiler may
+// fold the multiply that produced v into a mixed-precision v_mad_mix /
+// v_fma_mix with an f16 result, rounding once instead of f32-then-f16 as the
+// reference (and every other kernel here) does.
 AKAS_DEV uint32_t f32_to_f16_bits(float v) {
+  asm volatile("" : "+v"(v));
   _Float16 x = (_Float16)v;  // v_cvt_f16_f32: round to nearest even
   uint16_t b;
   __builtin_memcpy(&b, &x, 2);
@@ -157,6 +162,34 @@ AKAS_DEV float round_f16(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); 
 
 AKAS_DEV float round_to(float v, int dtype) {
   return dtype == AKAS_DTYPE_BF16 ? round_bf16(v) : (dtype == AKAS_DTYPE_F16 ? round_f16(v) : v);
+}
+
+// Compile-time-dtype rounding for unrolled epilogues: a runtime dtype inside
+// an unrolled loop costs a scalar branch per element.
+template <int DT>
+AKAS_DEV float round_t(float v) {
+  if constexpr (DT == AKAS_DTYPE_BF16)
+    return round_bf16(v);
+  else if constexpr (DT == AKAS_DTYPE_F16)
+    return round_f16(v);
+  else
+    return v;
+}
+
+template <int D>
+struct DtypeTag {
+  static constexpr int value = D;
+};
+
+// f(DtypeTag<d>{}) with the (wave-uniform) runtime dtype d made compile-time.
+template <class F>
+AKAS_DEV void with_dtype(int d, F&& f) {
+  if (d == AKAS_DTYPE_BF16)
+    f(DtypeTag<AKAS_DTYPE_BF16>{});
+  else if (d == AKAS_DTYPE_F16)
+    f(DtypeTag<AKAS_DTYPE_F16>{});
+  else
+    f(DtypeTag<AKAS_DTYPE_F32>{});
 }
 
 // Element load of a float-like buffer (f32 / f16 / bf16).
@@ -195,9 +228,31 @@ AKAS_DEV float load_scale_t(const void* p, int64_t i) {
 // (src/akas/ops/activation/kernel.py:83-88).  One definition shared by the
 // fused and the separate kernels so their results are bit-identical.
 // ---------------------------------------------------------------------------
+//
+// exp(-g) = 2^t with t = -g * log2(e) formed as a rounded head t0 plus the
+// tail recovered by FMA (Cody-Waite style argument splitting, log2(e) held as
+// a float head + float tail), so the argument carries ~1 ulp of error even
+// for large |g|; 2^t0 comes from v_exp_f32 and the tail is applied as
+// 2^t0 * (1 + tail * ln 2) (a product, not an FMA, so an overflowed 2^t0
+// stays +inf instead of inf - inf).  1 / (1 + e) uses v_rcp_f32.  The result is
+// within a few float ulp of g / (1 + exp(-g)) * u -- well inside the
+// reference's 2e-6 relative code band -- at about a tenth of the cost of
+// expf plus a correctly rounded division.
 AKAS_DEV float swiglu_elem(float g, float u) {
-  float d = 1.0f + expf(-g);
-  return __fdiv_rn(g, d) * u;
+  // Every fused multiply-add below is explicit: automatic contraction would
+  // depend on the surrounding code and could round the fused and the
+  // separate kernels differently.
+#pragma clang fp contract(off)
+  constexpr float kLog2eHi = 1.44269502162933349609375f;   // float(log2 e)
+  constexpr float kLog2eLo = 1.925963033500011079e-8f;     // log2 e - kLog2eHi
+  constexpr float kLn2 = 0.693147180559945309f;
+  const float x = -g;
+  const float t0 = x * kLog2eHi;
+  const float tail = __builtin_fmaf(x, kLog2eLo, __builtin_fmaf(x, kLog2eHi, -t0));
+  const float p = __builtin_amdgcn_exp2f(t0);
+  const float e = p * (1.0f + tail * kLn2);  // stays +inf when 2^t0 overflows
+  const float sig = __builtin_amdgcn_rcpf(1.0f + e);
+  return g * sig * u;
 }
 
 // ---------------------------------------------------------------------------

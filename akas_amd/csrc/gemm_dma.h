@@ -66,8 +66,8 @@ AKAS_DEV int piece_row(int wave, int i, int lane) { return ((wave & 3) * 8 + i) 
 // Byte offset within a source row of the chunk this lane fetches for tile row `row`.
 AKAS_DEV int piece_chunk(int row, int lane) { return ((lane & 7) ^ swizzle(row)) << 4; }
 
-// Per-wave copy plans.  offset(i) is the byte offset (k-block 0), relative
-// to src, of the 16 bytes this lane copies for piece i; rows past an
+// Per-wave copy plans.  ptr(i, ko) is the address of the 16 bytes this lane
+// copies for piece i of the k-block at byte offset ko; rows past an
 // operand's end are clamped to a valid row (their products are never stored).
 //
 // AffinePlan: the wave's source rows are row0 + 8*i (+ lane/8 folded into
@@ -85,24 +85,34 @@ struct AffinePlan {
   const float* as;      // activation scales (waves 0-3)
   uint32_t soff;        // this lane's activation-scale offset (row * KB)
   bool scales;          // wave copies activation scales
-  AKAS_DEV uint32_t offset(int i) const { return min(row0 + 8u * i, lim) * ld + (chunk ^ ((i & 1) << 4)); }
+  AKAS_DEV const uint8_t* ptr(int i, uint32_t ko) const {
+    return src + (min(row0 + 8u * i, lim) * ld + (chunk ^ ((i & 1) << 4)) + ko);
+  }
 };
 
 // GatherPlan: one arbitrary source offset per piece (rows gathered through
-// a route table).
+// a route table, or weight rows of two banks); piece i reads from
+// src + alt_delta instead of src when bit i of the wave-uniform alt_mask is
+// set.  (The bank is chosen by adding an integer, not by selecting between
+// two pointer fields, which would keep the plan in scratch memory.)
 struct GatherPlan {
   const uint8_t* src;
+  int64_t alt_delta;
+  uint32_t alt_mask;
   uint32_t off[8];
   int blk0;
   const float* as;
   uint32_t soff;
   bool scales;
-  AKAS_DEV uint32_t offset(int i) const { return off[i]; }
+  AKAS_DEV const uint8_t* ptr(int i, uint32_t ko) const {
+    const int64_t bank = ((alt_mask >> i) & 1u) ? alt_delta : 0;
+    return src + bank + (off[i] + ko);
+  }
 };
 
 template <int S, class Plan>
 AKAS_DEV void copy_piece(const Plan& p, int i, uint32_t ko) {
-  __builtin_amdgcn_global_load_lds((const void*)(p.src + (p.offset(i) + ko)),
+  __builtin_amdgcn_global_load_lds((const void*)p.ptr(i, ko),
                                    (lds_void*)(stage_base<S>() + (p.blk0 + i) * 1024), 16, 0, 0);
 }
 template <int S, class Plan>

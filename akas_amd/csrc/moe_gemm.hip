@@ -15,6 +15,7 @@
 // bit-identical to two expert_partial calls and the fused codes to
 // expert_partial x2 -> swiglu_experts -> quantize.
 #include "gemm_core.h"
+#include "gemm_dma.h"
 
 namespace akas {
 
@@ -207,19 +208,30 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
     // 128 activation columns of the tile (16 lanes x NT/2 tiles x WAVES_N).
     float act[MT][NT / 2][4];
     float rmax[MT][4];
+    with_dtype(p.prod_dtype, [&](auto PD) __attribute__((always_inline)) {
+      with_dtype(p.act_dtype, [&](auto AD) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4) {
+            float m = 0.f;
+#pragma unroll
+            for (int j = 0; j < NT / 2; ++j) {
+              const float g = round_t<decltype(PD)::value>(acc.t[i][2 * j][e4]);
+              const float u = round_t<decltype(PD)::value>(acc.t[i][2 * j + 1][e4]);
+              const float a = round_t<decltype(AD)::value>(swiglu_elem(g, u));
+              act[i][j][e4] = a;
+              m = __builtin_fmaxf(m, __builtin_fabsf(a));
+            }
+            rmax[i][e4] = m;
+          }
+      });
+    });
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
-        float m = 0.f;
-#pragma unroll
-        for (int j = 0; j < NT / 2; ++j) {
-          const float g = round_to(acc.t[i][2 * j][e4], p.prod_dtype);
-          const float u = round_to(acc.t[i][2 * j + 1][e4], p.prod_dtype);
-          const float a = round_to(swiglu_elem(g, u), p.act_dtype);
-          act[i][j][e4] = a;
-          m = __builtin_fmaxf(m, __builtin_fabsf(a));
-        }
+        float m = rmax[i][e4];
 #pragma unroll
         for (int o = 8; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o, 16));
         rmax[i][e4] = m;
@@ -254,6 +266,144 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
 }
 
 // ---------------------------------------------------------------------------
+// Prefill-sized experts: 256-row tiles on the DMA-fed 256x256 tile engine
+// (gemm_dma.h).  Waves 0-3 gather their A rows through the tile's route
+// table; waves 4-7 copy weight rows (MODE 1: gate rows for pieces 0,1,4,5
+// and up rows for pieces 2,3,6,7, i.e. 16-row gate/up tiles interleaved).
+// Work items are walked column block fastest, so a row tile's activations
+// stay in L2 across its column blocks and neighbouring row tiles of one
+// expert share its weights.
+// ---------------------------------------------------------------------------
+template <int MODE, int OUT, int SDT>
+__global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) {
+  constexpr bool PAIRED = MODE == 1;
+  constexpr int BM = dma::BM;
+  __shared__ int rows_src[BM];
+  __shared__ int rows_dst[BM];
+  __shared__ float row_max[PAIRED ? 2 : 1][PAIRED ? BM : 1];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int id = xcd_remap(blockIdx.x, p.max_tiles * p.tiles_n);
+  const int nb = id % p.tiles_n, t = id / p.tiles_n;
+  int e, tile;
+  locate_tile(p.counts, p.E, BM, t, lane, e, tile);
+  if (e < 0) return;  // uniform across the workgroup
+  const int count = min(p.counts[e], p.r);
+  const int row0 = tile * BM;
+  if (row0 >= count) return;  // only reachable with counts[e] > r
+  const int n0 = nb * (PAIRED ? dma::BN / 2 : dma::BN);
+  const int part = blockIdx.y;
+  const int KB = p.K / kBlock, NB = (p.N + kBlock - 1) / kBlock;
+  const int kb0 = part * p.kb_per_part, kb1 = kb0 + p.kb_per_part;
+
+  for (int i = tid; i < BM; i += dma::THREADS) {
+    const int idx = row0 + i;
+    const bool live = idx < count;
+    rows_src[i] = source_row(p, e, live ? idx : row0);
+    int dst = -1;
+    if (live) dst = p.packed_out ? p.offsets[e] + idx : p.routes[(int64_t)e * p.r + idx];
+    rows_dst[i] = dst < p.out_rows ? dst : -1;
+  }
+  __syncthreads();
+
+  dma::GatherPlan plan;
+  plan.blk0 = wave * 8;
+  plan.as = p.as;
+  if (wave < 4) {
+    plan.src = p.x;
+    plan.alt_delta = 0;
+    plan.alt_mask = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = dma::piece_row(wave, i, lane);
+      plan.off[i] = (uint32_t)rows_src[row] * (uint32_t)p.K + dma::piece_chunk(row, lane);
+    }
+    plan.soff = (uint32_t)rows_src[(wave & 3) * 64 + lane] * (uint32_t)KB;
+    plan.scales = true;
+  } else {
+    const int64_t ebase = (int64_t)e * p.N * p.K;
+    plan.src = p.w + ebase;
+    plan.alt_delta = PAIRED ? (int64_t)(p.w2 - p.w) : 0;
+    plan.alt_mask = PAIRED ? 0xCCu : 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rho = dma::piece_row(wave, i, lane);
+      const int col = PAIRED ? n0 + (rho >> 5) * 16 + (rho & 15) : n0 + rho;
+      plan.off[i] = (uint32_t)col * (uint32_t)p.K + dma::piece_chunk(rho, lane);
+    }
+    plan.soff = 0;
+    plan.scales = false;
+  }
+
+  const int wm = wave & 3, wn = wave >> 2;
+  const int a_row0 = wm * 64, b_row0 = wn * 128;
+  // First output column of this wave; gate and up share its scale block.
+  const int wcol = PAIRED ? n0 + b_row0 / 2 : n0 + b_row0;
+  const int64_t ws_base = ((int64_t)e * NB + wcol / kBlock) * KB;
+  dma::Acc acc;
+  acc.clear();
+  dma::run<PAIRED>(plan, acc, a_row0, b_row0, kb0, kb1, lane, [&](int kb) {
+    return float2{load_scale_t<SDT>(p.ws, ws_base + kb), PAIRED ? load_scale_t<SDT>(p.ws2, ws_base + kb) : 0.f};
+  });
+
+  if constexpr (!PAIRED) {
+    const int64_t rstride = (int64_t)p.parts * p.N;
+    dma::store_tile<OUT>(
+        acc, p.out, wave, lane, [&](int r) { return rows_dst[a_row0 + r] >= 0; },
+        [&](int r) { return (int64_t)rows_dst[a_row0 + r] * rstride + (int64_t)part * p.N + wcol; });
+  } else {
+    // Lane l holds, for m-tile i and column group c (0..3), gate in n-tile
+    // 2c and up in n-tile 2c+1 of row a_row0 + 16i + l%16 at output columns
+    // wcol + 16c + 4*(l/16) + 0..3.  SwiGLU in place of the gate values, then
+    // the row maximum over the tile's 128 output columns: 16 per lane group,
+    // 4 lane groups (xor 16, 32), 2 waves (LDS).
+    float rmax[4];
+    with_dtype(p.prod_dtype, [&](auto PD) __attribute__((always_inline)) {
+      with_dtype(p.act_dtype, [&](auto AD) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float m = 0.f;
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float g = round_t<decltype(PD)::value>(acc.t[i][2 * c][q]);
+              const float u = round_t<decltype(PD)::value>(acc.t[i][2 * c + 1][q]);
+              const float a = round_t<decltype(AD)::value>(swiglu_elem(g, u));
+              acc.t[i][2 * c][q] = a;
+              m = __builtin_fmaxf(m, __builtin_fabsf(a));
+            }
+          rmax[i] = m;
+        }
+      });
+    });
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float m = __builtin_fmaxf(rmax[i], __shfl_xor(rmax[i], 16, 64));
+      m = __builtin_fmaxf(m, __shfl_xor(m, 32, 64));
+      if (lane < 16) row_max[wn][a_row0 + 16 * i + lane] = m;
+    }
+    __syncthreads();
+    uint8_t* codes = reinterpret_cast<uint8_t*>(p.out);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = a_row0 + 16 * i + (lane & 15);
+      const GroupScale gs = make_group_scale(__builtin_fmaxf(row_max[0][r], row_max[1][r]));
+      const int dst = rows_dst[r];
+      if (dst < 0) continue;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const v4f& a = acc.t[i][2 * c];
+        *reinterpret_cast<uint32_t*>(codes + (int64_t)dst * p.N + wcol + 16 * c + 4 * (lane >> 4)) =
+            e4m3_encode4_scaled(a[0], a[1], a[2], a[3], gs);
+      }
+      if (wn == 0 && lane < 16) p.out_scales[(int64_t)dst * (p.N / kBlock) + n0 / kBlock] = gs.s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // launch
 // ---------------------------------------------------------------------------
 
@@ -274,13 +424,32 @@ static void launch_expert(ExpertArgs a, hipStream_t s) {
     expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_BF16><<<grid, 64 * WMW * WNW, 0, s>>>(a);
 }
 
+template <int MODE, int OUT>
+static void launch_expert_dma(ExpertArgs a, hipStream_t s) {
+  a.max_tiles = (int)capacity_tiles(a.r, a.top, a.E, dma::BM);
+  a.tiles_n = MODE == 1 ? a.N / (dma::BN / 2) : a.N / dma::BN;
+  dim3 grid((unsigned)(a.max_tiles * a.tiles_n), (unsigned)a.parts);
+  if (a.ws_dtype == AKAS_DTYPE_F32)
+    expert_dma_kernel<MODE, OUT, AKAS_DTYPE_F32><<<grid, dma::THREADS, 0, s>>>(a);
+  else
+    expert_dma_kernel<MODE, OUT, AKAS_DTYPE_BF16><<<grid, dma::THREADS, 0, s>>>(a);
+}
+
+// Experts holding hundreds of rows on average (prefill batches) take the
+// DMA-fed 256-row tiles; its 16-byte stores need a 16-byte aligned output.
+static bool expert_dma_fits(const ExpertArgs& a, int64_t mean, int64_t n_mult) {
+  return mean >= 128 && a.N % n_mult == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0;
+}
+
 // Row tile by the mean rows per expert: 32-row tiles for decode-like batches,
-// 128-row tiles once experts hold hundreds of rows.
+// 128-row tiles in between, DMA-fed 256-row tiles for prefill batches.
 template <int OUT>
 static void launch_partial(const ExpertArgs& a, hipStream_t s) {
   const int64_t mean = (int64_t)a.r * a.top / a.E;
   if (mean <= 48)
     launch_expert<32, 128, 1, 4, 0, OUT>(a, s);
+  else if (expert_dma_fits(a, mean, dma::BN))
+    launch_expert_dma<0, OUT>(a, s);
   else
     launch_expert<128, 128, 2, 2, 0, OUT>(a, s);
 }
@@ -289,6 +458,8 @@ static void launch_swiglu(const ExpertArgs& a, hipStream_t s) {
   const int64_t mean = (int64_t)a.r * a.top / a.E;
   if (mean <= 48)
     launch_expert<32, 256, 1, 4, 1, AKAS_DTYPE_F32>(a, s);
+  else if (expert_dma_fits(a, mean, dma::BN / 2))
+    launch_expert_dma<1, AKAS_DTYPE_F32>(a, s);
   else
     launch_expert<128, 256, 2, 4, 1, AKAS_DTYPE_F32>(a, s);
 }

@@ -177,7 +177,10 @@ def _expert_case(rng, rows, top, experts, o, k, routed, exact=True, mult=1):
 @pytest.mark.parametrize("rows,top,experts,o,k,routed", [
     (3, 2, 4, 128, 256, False), (1, 4, 64, 128, 256, False), (33, 2, 4, 128, 256, False),
     (33, 2, 4, 128, 384, True), (257, 3, 7, 256, 384, True), (256, 4, 64, 256, 512, False),
-    (2048, 4, 8, 256, 256, False)])
+    (2048, 4, 8, 256, 256, False),
+    # >= 128 rows per expert: 256-row DMA tiles (ragged last tiles, gathered
+    # and routed rows, N = 256 and 512, and N = 384 on the 128-row fallback)
+    (1500, 2, 6, 512, 384, True), (700, 4, 16, 256, 512, False), (600, 3, 5, 384, 256, False)])
 def test_expert_partial_exact(dev, rows, top, experts, o, k, routed):
     from akas_amd import ops
 
@@ -189,14 +192,15 @@ def test_expert_partial_exact(dev, rows, top, experts, o, k, routed):
     np.testing.assert_array_equal(_np(out), exp)
 
 
+@pytest.mark.parametrize("rows", [257, 1200])
 @pytest.mark.parametrize("out_dtype", ["float32", "bfloat16", "float16"])
 @pytest.mark.parametrize("scale_dtype", ["float32", "bfloat16"])
-def test_expert_partial_random_dtypes(dev, out_dtype, scale_dtype):
+def test_expert_partial_random_dtypes(dev, rows, out_dtype, scale_dtype):
     import torch
     from akas_amd import ops
 
     rng = np.random.default_rng(41)
-    rows, top, experts, o, k = 257, 3, 7, 256, 384
+    top, experts, o, k = 3, 7, 256, 384
     ids, active, counts, routes, x, xs, w, ws = _expert_case(rng, rows, top, experts, o, k, False,
                                                              exact=False, mult=3)
     sdt = getattr(torch, scale_dtype)
@@ -207,11 +211,12 @@ def test_expert_partial_random_dtypes(dev, out_dtype, scale_dtype):
     assert rel_fro(_np(out), exp) < (1e-4 if out_dtype == "float32" else 4e-3)
 
 
-def test_expert_partial_partitions_and_merge(dev):
+@pytest.mark.parametrize("rows,o", [(33, 128), (600, 256)])
+def test_expert_partial_partitions_and_merge(dev, rows, o):
     from akas_amd import ops
 
     rng = np.random.default_rng(43)
-    rows, top, experts, o, k = 33, 2, 4, 128, 512
+    top, experts, k = 2, 4, 512
     ids, active, counts, routes, x, xs, w, ws = _expert_case(rng, rows, top, experts, o, k, False)
     out = ops.expert_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev), _t(counts, dev),
                              _t(routes, dev), r=rows, top=top, partitions=2)
@@ -221,12 +226,13 @@ def test_expert_partial_partitions_and_merge(dev):
     np.testing.assert_array_equal(_np(merged), omoe.expert_merge(exp))
 
 
+@pytest.mark.parametrize("rows,maxm", [(33, 64), (600, 128)])
 @pytest.mark.parametrize("routed", [False, True])
-def test_expert_partial_packed_input(dev, routed):
+def test_expert_partial_packed_input(dev, routed, rows, maxm):
     from akas_amd import ops
 
     rng = np.random.default_rng(47)
-    rows, top, experts, o, k, maxm = 33, 3, 7, 256, 384, 64
+    top, experts, o, k = 3, 7, 256, 384
     ids, active, counts, routes, x, xs, w, ws = _expert_case(rng, rows, top, experts, o, k, routed)
     te, tr = omoe.expert_tile_map(counts, rows, top, maxm)
     px, pxs, offs = omoe.expert_pack(x, xs, counts, routes, top, experts, maxm, routed)
@@ -243,7 +249,10 @@ SWIGLU_CASES = [(1, 3, 7, 128, 256, "float32", "float32"),
                 (33, 3, 7, 256, 384, "float16", "float16"),
                 (257, 3, 7, 256, 384, "bfloat16", "bfloat16"),
                 (256, 4, 64, 256, 512, "bfloat16", "bfloat16"),
-                (2048, 4, 8, 256, 256, "float32", "bfloat16")]
+                (2048, 4, 8, 256, 256, "float32", "bfloat16"),
+                # >= 128 rows per expert: 256-row DMA tiles
+                (1200, 3, 7, 256, 384, "bfloat16", "bfloat16"),
+                (900, 2, 5, 384, 256, "float32", "float32")]
 
 
 @pytest.mark.parametrize("rows,top,experts,o,k,pd,ad", SWIGLU_CASES)
@@ -317,13 +326,14 @@ def test_fused_swiglu_exact_products_midpoint_band(dev, rows, top, experts, o, k
     np.testing.assert_allclose(_np(scales)[live], osc[live], rtol=2e-6, atol=1e-12)
 
 
+@pytest.mark.parametrize("rows,maxm", [(33, 64), (700, 128)])
 @pytest.mark.parametrize("pd,ad", [("float32", "float32"), ("bfloat16", "bfloat16")])
-def test_fused_swiglu_packed_in_out(dev, pd, ad):
+def test_fused_swiglu_packed_in_out(dev, pd, ad, rows, maxm):
     import torch
     from akas_amd import ops
 
     rng = np.random.default_rng(1035)
-    rows, top, experts, o, k, maxm = 33, 3, 7, 256, 384, 64
+    top, experts, o, k = 3, 7, 256, 384
     ids, active = pattern_routes(rows, top, experts, 3)
     counts, routes = omoe.quantized_routes(ids, active, experts)
     x = random_codes(rng, (rows, k))
@@ -366,6 +376,23 @@ def test_swiglu_experts(dev, parts):
     out = ops.swiglu_experts(_t(g, dev), _t(u, dev), round_inputs=True, round_dtype="bfloat16")
     exp = omoe.swiglu_experts(g, u, round_inputs=True, round_dtype="bfloat16")
     np.testing.assert_allclose(_np(out), exp, rtol=2e-6, atol=1e-7)
+
+
+def test_swiglu_wide_range_accuracy(dev):
+    """g / (1 + exp(-g)) * u against a float64 evaluation over g in
+    [-104, 88] (exp(-g) from far above overflow to far below underflow),
+    within the reference's 2e-6 relative code band."""
+    from akas_amd import ops
+
+    rng = np.random.default_rng(11)
+    g = np.concatenate([np.linspace(-104, 88, 96 * 256), rng.normal(0, 8, 32 * 256)]).astype(np.float32)
+    u = rng.uniform(0.5, 2.0, g.size).astype(np.float32) * rng.choice([-1, 1], g.size).astype(np.float32)
+    shape = (g.size // 256, 1, 256)
+    out = _np(ops.swiglu_experts(_t(g.reshape(shape), dev), _t(u.reshape(shape), dev))).ravel()
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    with np.errstate(over="ignore"):
+        exact = g64 / (1.0 + np.exp(-g64)) * u64
+    np.testing.assert_allclose(out, exact, rtol=2e-6, atol=1e-30)
 
 
 @pytest.mark.parametrize("in_dtype", ["float32", "bfloat16"])
