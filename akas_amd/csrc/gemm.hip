@@ -2,6 +2,7 @@
 // (prefill) MFMA kernels, split-K partials and the partition merge.
 #include "gemm_core.h"
 #include "gemm_dma.h"
+#include "quant_group.h"
 
 namespace akas {
 
@@ -16,6 +17,8 @@ struct DenseArgs {
   int M, N, K;
   int kb_per_part;      // k-blocks per partition
   int ws_dtype, out_dtype;
+  const void* x;        // unquantized activations [M, K] (kernels that quantize while staging)
+  int x_dtype;
 };
 
 // Logical tile id -> (tm, tn): groups of G m-tiles walked n-major so that a
@@ -322,7 +325,13 @@ constexpr size_t wide_lds_bytes(int kbp) {
   return stage > red ? stage : red;
 }
 
-template <int MT, int NTW, int KS, int OUT, int SDT>
+//
+// QX = 0: the slab is staged from prequantized codes and scales (a, as).
+// QX = DT + 1: the slab is quantized from the f32/f16/bf16 activations x
+// while it is staged -- 16 lanes per 1x128 group, the same quantize8 as the
+// standalone quantizer, so the codes are identical -- which saves the
+// quantizer's launch and its codes' round trip for decode-sized batches.
+template <int MT, int NTW, int KS, int OUT, int SDT, int QX = 0>
 __global__ __launch_bounds__(64 * NTW * KS) void dense_wide_kernel(DenseArgs p) {
   constexpr int THREADS = 64 * NTW * KS;
   constexpr int ROWS = 16 * MT;
@@ -357,16 +366,51 @@ __global__ __launch_bounds__(64 * NTW * KS) void dense_wide_kernel(DenseArgs p) 
   issue(0);
 
   // 2. stage the activation slab (rows past M are zero) and its scales
-  for (int c = tid; c < ROWS * kbp * 8; c += THREADS) {
-    const int row = c / (kbp * 8), rem = c % (kbp * 8), lk = rem >> 3, ch = rem & 7;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (row < p.M)
-      v = *reinterpret_cast<const u32x4*>(p.a + (int64_t)row * p.K + (int64_t)(kb0 + lk) * kBlock + ch * 16);
-    *reinterpret_cast<u32x4*>(lds_a + (size_t)lk * ROWS * 128 + lds_off(row, ch)) = v;
-  }
-  for (int c = tid; c < ROWS * kbp; c += THREADS) {
-    const int lk = c / ROWS, row = c % ROWS;
-    lds_s[c] = row < p.M ? p.as[(int64_t)row * KB + kb0 + lk] : 0.f;
+  if constexpr (QX == 0) {
+    for (int c = tid; c < ROWS * kbp * 8; c += THREADS) {
+      const int row = c / (kbp * 8), rem = c % (kbp * 8), lk = rem >> 3, ch = rem & 7;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (row < p.M)
+        v = *reinterpret_cast<const u32x4*>(p.a + (int64_t)row * p.K + (int64_t)(kb0 + lk) * kBlock + ch * 16);
+      *reinterpret_cast<u32x4*>(lds_a + (size_t)lk * ROWS * 128 + lds_off(row, ch)) = v;
+    }
+    for (int c = tid; c < ROWS * kbp; c += THREADS) {
+      const int lk = c / ROWS, row = c % ROWS;
+      lds_s[c] = row < p.M ? p.as[(int64_t)row * KB + kb0 + lk] : 0.f;
+    }
+  } else {
+    // rows past M: zero codes and scales, no loads
+    for (int c = p.M * kbp * 8 + tid; c < ROWS * kbp * 8; c += THREADS) {
+      const int row = c / (kbp * 8), rem = c % (kbp * 8), lk = rem >> 3, ch = rem & 7;
+      *reinterpret_cast<u32x4*>(lds_a + (size_t)lk * ROWS * 128 + lds_off(row, ch)) = u32x4{0u, 0u, 0u, 0u};
+    }
+    for (int c = tid; c < ROWS * kbp; c += THREADS)
+      if (c % ROWS >= p.M) lds_s[c] = 0.f;
+    // live groups (row, lk), one per 16 lanes, PASS groups per lane block with
+    // all their loads issued before any is used; lane l16 holds values
+    // 8*l16 .. 8*l16+7, i.e. half (l16 & 1) of chunk l16 / 2
+    constexpr int GPP = THREADS / 16, PASS = 4;
+    const int l16 = lane & 15, groups = p.M * kbp;
+    for (int c0 = tid >> 4; c0 < groups; c0 += PASS * GPP) {
+      float v[PASS][8];
+#pragma unroll
+      for (int u = 0; u < PASS; ++u) {
+        const int c = c0 + u * GPP;
+        if (c < groups)
+          load8<QX - 1>(p.x, (int64_t)(c / kbp) * p.K + (int64_t)(kb0 + c % kbp) * kBlock + l16 * 8, v[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < PASS; ++u) {
+        const int c = c0 + u * GPP;
+        if (c < groups) {  // uniform across the group's 16 lanes
+          const int row = c / kbp, lk = c % kbp;
+          float sc;
+          const uint2 codes = quantize8(v[u], sc);
+          *reinterpret_cast<uint2*>(lds_a + (size_t)lk * ROWS * 128 + lds_off(row, l16 >> 1) + (l16 & 1) * 8) = codes;
+          if (l16 == 0) lds_s[lk * ROWS + row] = sc;
+        }
+      }
+    }
   }
   __syncthreads();
 
@@ -473,11 +517,11 @@ static void launch_small(const DenseArgs& a, int parts, hipStream_t s) {
     dense_small_kernel<4, OUT, SDT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
 }
 
-template <int MT, int NTW, int KS, int OUT, int SDT>
+template <int MT, int NTW, int KS, int OUT, int SDT, int QX = 0>
 static bool launch_wide(const DenseArgs& a, int parts, hipStream_t s) {
   const size_t lds = wide_lds_bytes<MT, NTW, KS>(a.kb_per_part);
   if (lds > 160 * 1024 || a.N % (16 * NTW)) return false;
-  auto kern = dense_wide_kernel<MT, NTW, KS, OUT, SDT>;
+  auto kern = dense_wide_kernel<MT, NTW, KS, OUT, SDT, QX>;
   static bool configured = false;  // attribute set once per instantiation
   if (!configured) {
     hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -544,6 +588,43 @@ int launch_dense(const DenseArgs& a, int parts, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? AKAS_OK : AKAS_ERR_LAUNCH;
 }
 
+// Decode-sized fp8_linear in one launch: the wide kernel quantizes x while
+// staging it.  False when the shape does not fit the wide kernel.
+// Up to kFusedQuantizeRows rows: beyond that every workgroup re-quantizing
+// the whole slab costs more than the separate quantizer's launch (decode
+// sweep, K=2048, N=6144: fused 5.1 / 6.3 us vs 7.5 / 7.9 us at M=1 / 4, but
+// 9.2 vs 8.3 us at M=16).
+constexpr int kFusedQuantizeRows = 8;
+
+template <int OUT, int SDT, int QX>
+static bool launch_fused_small_t(const DenseArgs& a, hipStream_t s) {
+  if (a.M <= 16) return launch_wide<1, 2, 8, OUT, SDT, QX>(a, 1, s);
+  return false;
+}
+
+template <int OUT, int SDT>
+static bool launch_fused_small_o(const DenseArgs& a, hipStream_t s) {
+  switch (a.x_dtype) {
+    case AKAS_DTYPE_F32: return launch_fused_small_t<OUT, SDT, AKAS_DTYPE_F32 + 1>(a, s);
+    case AKAS_DTYPE_F16: return launch_fused_small_t<OUT, SDT, AKAS_DTYPE_F16 + 1>(a, s);
+    default: return launch_fused_small_t<OUT, SDT, AKAS_DTYPE_BF16 + 1>(a, s);
+  }
+}
+
+template <int OUT>
+static bool launch_fused_small_s(const DenseArgs& a, hipStream_t s) {
+  return a.ws_dtype == AKAS_DTYPE_F32 ? launch_fused_small_o<OUT, AKAS_DTYPE_F32>(a, s)
+                                      : launch_fused_small_o<OUT, AKAS_DTYPE_BF16>(a, s);
+}
+
+static bool launch_fused_small(const DenseArgs& a, hipStream_t s) {
+  switch (a.out_dtype) {
+    case AKAS_DTYPE_F32: return launch_fused_small_s<AKAS_DTYPE_F32>(a, s);
+    case AKAS_DTYPE_BF16: return launch_fused_small_s<AKAS_DTYPE_BF16>(a, s);
+    default: return launch_fused_small_s<AKAS_DTYPE_F16>(a, s);
+  }
+}
+
 static inline bool float_dtype(int d) {
   return d == AKAS_DTYPE_F32 || d == AKAS_DTYPE_F16 || d == AKAS_DTYPE_BF16;
 }
@@ -574,13 +655,20 @@ extern "C" int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, con
   if (!x || !w || !w_scales || !out) return AKAS_ERR_NULL;
   if (!workspace || workspace_bytes < akas_fp8_linear_workspace_size(r, k, o))
     return AKAS_ERR_WORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (r <= kFusedQuantizeRows) {
+    DenseArgs f{nullptr, nullptr, w, w_scales, out, o, 0, (int)r, (int)o, (int)k,
+                (int)(k / kBlock), scale_dtype, out_dtype, x, x_dtype};
+    if (launch_fused_small(f, s))
+      return hipGetLastError() == hipSuccess ? AKAS_OK : AKAS_ERR_LAUNCH;
+  }
   uint8_t* codes = reinterpret_cast<uint8_t*>(workspace);
   float* scales = reinterpret_cast<float*>(codes + align256((size_t)r * k));
   int st = akas_quantize(x, x_dtype, codes, scales, r, k, stream);
   if (st != AKAS_OK) return st;
   DenseArgs a{codes, scales, w, w_scales, out, o, 0, (int)r, (int)o, (int)k,
-              (int)(k / kBlock), scale_dtype, out_dtype};
-  return launch_dense(a, 1, reinterpret_cast<hipStream_t>(stream));
+              (int)(k / kBlock), scale_dtype, out_dtype, nullptr, 0};
+  return launch_dense(a, 1, s);
 }
 
 extern "C" int akas_projection_partial(const uint8_t* x, const float* activation_scales,

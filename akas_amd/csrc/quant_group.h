@@ -1,0 +1,50 @@
+// One 1x128 activation group quantized by 16 consecutive lanes (8 values
+// each): shared by the standalone quantizer and the GEMMs that quantize
+// their activation slab while staging it, so both produce the same codes.
+// (src/akas/quantization/activations/fp8/cuda.py:10-56, warp form :80-141)
+#pragma once
+
+#include "common.h"
+
+namespace akas {
+
+// 8 contiguous values of a float buffer of dtype DT, widened to f32.
+template <int DT>
+AKAS_DEV void load8(const void* x, int64_t base, float v[8]) {
+  if constexpr (DT == AKAS_DTYPE_F32) {
+    const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + base);
+    float4 a = p[0], b = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    uint4 w = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + base);
+    uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == AKAS_DTYPE_BF16) {
+        v[2 * i] = __uint_as_float(u[i] << 16);
+        v[2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
+      } else {
+        v[2 * i] = f16_bits_to_f32(u[i] & 0xFFFFu);
+        v[2 * i + 1] = f16_bits_to_f32(u[i] >> 16);
+      }
+    }
+  }
+}
+
+// Codes of this lane's 8 values (low word = values 0..3) and the group scale
+// max(max|x|, 1e-12) / 448, the maximum taken over the 16 lanes of the group
+// (lanes 16*i .. 16*i+15 of the wave, all active).
+AKAS_DEV uint2 quantize8(const float v[8], float& scale) {
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o, 16));
+  const GroupScale gs = make_group_scale(m);
+  scale = gs.s;
+  return make_uint2(e4m3_encode4_scaled(v[0], v[1], v[2], v[3], gs),
+                    e4m3_encode4_scaled(v[4], v[5], v[6], v[7], gs));
+}
+
+}  // namespace akas

@@ -7,32 +7,9 @@
 // codes as one 8-byte word.  Division by the group scale is the exact
 // correctly rounded quotient (common.h), so codes match the reference's IEEE
 // division bit for bit.
-#include "common.h"
+#include "quant_group.h"
 
 namespace akas {
-
-template <int DT>
-AKAS_DEV void load8(const void* x, int64_t base, float v[8]) {
-  if constexpr (DT == AKAS_DTYPE_F32) {
-    const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(x) + base);
-    float4 a = p[0], b = p[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  } else {
-    uint4 w = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + base);
-    uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (DT == AKAS_DTYPE_BF16) {
-        v[2 * i] = __uint_as_float(u[i] << 16);
-        v[2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
-      } else {
-        v[2 * i] = f16_bits_to_f32(u[i] & 0xFFFFu);
-        v[2 * i + 1] = f16_bits_to_f32(u[i] >> 16);
-      }
-    }
-  }
-}
 
 // One 128-group per 16 lanes; grid-stride over all groups.
 // (src/akas/quantization/activations/fp8/cuda.py:10-56, warp form :80-141)
@@ -46,18 +23,10 @@ __global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ 
   const int64_t stride = ((int64_t)gridDim.x * blockDim.x) >> 4;
   for (int64_t g = first; g < groups; g += stride) {
     const int64_t base = g * kBlock + lane16 * 8;
-    float v[8];
+    float v[8], s;
     load8<DT>(x, base, v);
-    float m = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o, 16));
-    const GroupScale gs = make_group_scale(m);
-    const uint32_t lo = e4m3_encode4_scaled(v[0], v[1], v[2], v[3], gs);
-    const uint32_t hi = e4m3_encode4_scaled(v[4], v[5], v[6], v[7], gs);
-    *reinterpret_cast<uint2*>(out + base) = make_uint2(lo, hi);
-    if (lane16 == 0) scales[g] = gs.s;
+    *reinterpret_cast<uint2*>(out + base) = quantize8(v, s);
+    if (lane16 == 0) scales[g] = s;
   }
 }
 

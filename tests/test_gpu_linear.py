@@ -82,6 +82,33 @@ def test_fp8_linear_decode_shapes(dev, m, scale_dtype):
     assert err < 1e-4, err
 
 
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64])
+@pytest.mark.parametrize("x_dtype", ["float32", "float16", "bfloat16"])
+def test_fp8_linear_fused_quantize_matches_two_step(dev, m, x_dtype):
+    """Up to 64 rows fp8_linear quantizes x inside the GEMM; the result is bit
+    for bit quantize -> projection_partial, and the in-kernel codes equal
+    the standalone quantizer's (stress rows included)."""
+    import torch
+    from akas_amd import ops
+    from golden_inputs import stress_rows
+
+    rng = np.random.default_rng(m)
+    codes, scales = block_weights(rng, (768, 2048))
+    x = np.concatenate([bf16_normal(rng, (max(m - 2, 1), 2048), outliers=0.01),
+                        stress_rows(2048, 2, rng)])[:m]
+    xt = _t(x, dev, getattr(torch, x_dtype))
+    w, s = _t(codes, dev), _t(scales, dev)
+    y = ops.fp8_linear(xt, w, s, out_dtype=torch.float32)
+    q, qs = ops.quantize(xt)
+    y2 = ops.projection_partial(q, qs, w, s, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), y2.cpu().numpy())
+    xq = ofp8.round_to(x, x_dtype)
+    ec, es = ofp8.quantize(xq)
+    np.testing.assert_array_equal(q.cpu().numpy(), ec)
+    assert rel_fro(y.cpu().numpy(), ofp8.fp8_linear(xq, codes, scales)) < 1e-4
+
+
 @pytest.mark.parametrize("out_dtype", ["float32", "bfloat16", "float16"])
 def test_fp8_linear_config1_and_out_dtypes(dev, out_dtype):
     """Config: x bf16 [16,2048] ~N(0,1), W N(0,0.02) block-quantized, seed 0."""
