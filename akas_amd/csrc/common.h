@@ -265,8 +265,10 @@ AKAS_DEV float swiglu_elem(float g, float u) {
 //   B operand: lane l holds the same 32 k-bytes of column (l % 16).
 //   D:         lane l, element i holds row 4*(l/16) + i, column l % 16.
 // The instruction sums matching (lane group, byte) positions of A and B, so
-// any consistent assignment of k to (g, byte) gives the same product; the
-// layout above is verified on the device by tests/test_gpu_mfma_layout.py.
+// any consistent assignment of k to (g, byte) gives the same product.  The
+// row/column assignment of D is verified on the device by the exact-product
+// tests with distinct per-row and per-block scales in tests/test_gpu_linear.py
+// (a misplaced row or column lands on a different scale and fails them).
 // The scaled MFMA with unit E8M0 scales (127) is the plain FP8 product;
 // format code 0 selects OCP e4m3 for both operands.
 AKAS_DEV v4f mfma_e4m3(const v8i& a, const v8i& b) {

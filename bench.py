@@ -16,6 +16,7 @@ GB/s; ``roofline`` for the dominant kernel (HIP-event timing of that kernel
 alone); ``cpu_baseline`` from the oracle's C restatement on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--no-extras] [--no-cpu]
+    python bench.py --kernel-probe    # launches for rocprofv3 --pmc passes
 """
 
 import argparse
@@ -286,6 +287,52 @@ def cpu_baseline(budget_s=12.0):
                        f"-fopenmp f32 accumulation")
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_gemm_m256_counters.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant decode GEMM from the committed
+    FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy of known
+    size), or None when the summary is absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+PROBE_M = 256          # the sweep's dominant GEMM (largest kernel time)
+PROBE_COPY_BYTES = 256 << 20
+
+
+def kernel_probe(torch, dev):
+    """Launches for hardware-counter runs: the dominant decode GEMM (M=256,
+    prequantized input, bf16 out, each launch on a different weight copy) 20
+    times, then a plain 256 MiB device copy 5 times, whose FETCH_SIZE /
+    WRITE_SIZE calibrate the counters against a known byte count."""
+    from akas_amd import ops
+
+    copies = 20
+    codes, scales = make_weights(torch, N_DEC, K_DEC, copies, 1234, dev)
+    x = bf16_activations(torch, PROBE_M, K_DEC, PROBE_M, dev)
+    q, qs = ops.quantize(x)
+    out = torch.empty((PROBE_M, N_DEC), dtype=torch.bfloat16, device=dev)
+    for i in range(copies):
+        ops.projection_partial(q, qs, codes[i], scales[i], out=out, out_dtype=torch.bfloat16)
+    src = torch.empty(PROBE_COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps(dict(probe="decode GEMM M=256 K=2048 N=6144 x20, then 256 MiB copy x5",
+                          gemm_bytes_per_launch=gemm_kernel_bytes(PROBE_M, K_DEC, N_DEC),
+                          copy_bytes=PROBE_COPY_BYTES)))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -293,6 +340,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-probe", action="store_true",
+                    help="only launch the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported "
@@ -306,15 +355,20 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.kernel_probe:
+        kernel_probe(torch, dev)
+        return
 
     dec = decode_sweep(torch, dev, args.steps, args.warmup)
     value = dec["step_bytes"] / dec["step_s"] / 1e9
     # dominant kernel: the largest share of the sweep's GEMM time
     dom = max(dec["per_m"], key=lambda r: r["kernel_us"])
+    traffic = measured_traffic() if dom["M"] == PROBE_M else None
     roofline = dict(bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(dom["gbs"] / HBM_PEAK_GBS, 4), traffic=None,
+                    frac=round(dom["gbs"] / HBM_PEAK_GBS, 4), traffic=traffic,
                     kernel=f"GEMM launch at M={dom['M']}, K={K_DEC}, N={N_DEC}",
-                    bytes_per_launch=dom["bytes"], avg_us=dom["kernel_us"])
+                    bytes_per_launch=dom["bytes"], avg_us=dom["kernel_us"],
+                    traffic_source=os.path.relpath(TRAFFIC_PROFILE, ROOT) if traffic else None)
     line = dict(metric=METRIC, value=round(value, 1), unit="GB/s", n_gpus=1, steps=dec["steps"],
                 warmup=args.warmup, ms_per_step=round(dec["step_s"] * 1e3, 4),
                 higher_is_better=True, scaling="weak", vs_baseline=None, dtype="fp8e4m3xfp8e4m3->f32",
