@@ -158,6 +158,225 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void dense_tiled_kernel(Den
 }
 
 // ---------------------------------------------------------------------------
+// Decode-shape GEMM, 16 < M <= 256: split-K across the waves of a workgroup
+//
+// At these sizes the weights are the only operand that comes from HBM and
+// the vector L1 is the other limit: at one workgroup per CU it passes about
+// 100-120 GB/s per CU when each load instruction covers whole 128-byte
+// lines (eight lanes per line), but only a third of that when sixteen rows
+// share one instruction -- which is what loading straight into the MFMA
+// operand order does.  So:
+//   * A workgroup owns a BM x BN output tile; its four waves split the
+//     k-range four ways.  Each wave stages its BN x 512-byte weight slice
+//     (two rows of 512 contiguous bytes per load instruction) in a private
+//     swizzled LDS region, requesting all of it up front, and reads MFMA
+//     fragments back with conflict-free 16-byte LDS reads.
+//   * Activations come either fragment-major (AF = 1: the quantizer in
+//     fp8_linear writes 2 KB tiles in which one contiguous 1 KB load per half
+//     is already in the MFMA lane order), or row-major (AF = 0, caller-owned
+//     codes): four neighbouring lanes per row, moved to the MFMA lane order
+//     with ds_bpermute.
+//   * The four partial tiles are summed in wave order through LDS.
+//
+// Lane r + 16g of an operand fragment holds 16-byte chunks g and 4+g of its
+// row's k-block (the k-assignment every path uses).  The product is taken
+// as D = W * A^T: lane l holds output row m0 + 16i + l%16 and columns
+// n0 + 16j + 4(l/16) .. +3, so one scale product per tile covers the lane's
+// four elements and the store is one vector.
+// ---------------------------------------------------------------------------
+struct RawFragment {
+  u32x4 lo, hi;
+};
+
+// Row-major operand: lane 4r+c reads chunks c and 4+c of row r.
+AKAS_DEV RawFragment load_raw_fragment(const uint8_t* row_kblock, int chunk) {
+  return {*reinterpret_cast<const u32x4*>(row_kblock + 16 * chunk),
+          *reinterpret_cast<const u32x4*>(row_kblock + 64 + 16 * chunk)};
+}
+
+// lane r + 16g takes lane 4r + g
+AKAS_DEV v8i to_mfma_order(const RawFragment& f, int sel) {
+  v8i v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = __builtin_amdgcn_ds_bpermute(sel, (int)f.lo[e]);
+    v[4 + e] = __builtin_amdgcn_ds_bpermute(sel, (int)f.hi[e]);
+  }
+  return v;
+}
+
+AKAS_DEV v8i as_fragment(const RawFragment& f) {
+  v8i v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = (int)f.lo[e];
+    v[4 + e] = (int)f.hi[e];
+  }
+  return v;
+}
+
+template <int DT>
+AKAS_DEV void store_out4(void* out, int64_t i, const v4f& v) {
+  if constexpr (DT == AKAS_DTYPE_F32) {
+    *reinterpret_cast<v4f*>(reinterpret_cast<float*>(out) + i) = v;
+  } else {
+    uint2 q;
+    if constexpr (DT == AKAS_DTYPE_BF16) {
+      q.x = f32x2_to_bf16x2(v[0], v[1]);
+      q.y = f32x2_to_bf16x2(v[2], v[3]);
+    } else {
+      q.x = f32_to_f16_bits(v[0]) | (f32_to_f16_bits(v[1]) << 16);
+      q.y = f32_to_f16_bits(v[2]) | (f32_to_f16_bits(v[3]) << 16);
+    }
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + i) = q;
+  }
+}
+
+constexpr int kSplitWaves = 4;
+constexpr int kSplitKbw = 4;  // k-blocks per wave: 2048-deep partitions
+
+template <int MT, int NT, int PF, int AF, int OUT, int SDT>
+__global__ __launch_bounds__(64 * kSplitWaves) void dense_split_kernel(DenseArgs p) {
+  constexpr int KBW = kSplitKbw, BM = 16 * MT, BN = 16 * NT, TILES = MT * NT;
+  constexpr int WROW = KBW * kBlock;                 // bytes of a weight row per wave
+  constexpr int WAVE_LDS = BN * WROW > TILES * kWave * 16 ? BN * WROW : TILES * kWave * 16;
+  static_assert(PF >= 1 && PF <= KBW, "activation prefetch depth");
+  static_assert(BN % 2 == 0 && WROW == 512, "two 512-byte weight rows per load");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kSplitWaves * WAVE_LDS];
+
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tiles_m = (p.M + BM - 1) / BM, tiles_n = p.N / BN;
+  // m-tiles of one column block are adjacent, so both reads of a weight
+  // slice land in the same XCD's L2
+  const int id = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+  const int tm = id % tiles_m, tn = id / tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int KB = p.K / kBlock;
+  const int part = blockIdx.y;
+  const int kb0 = part * p.kb_per_part + wave * KBW;
+  uint8_t* wlds = lds + wave * WAVE_LDS;
+
+  // Rows past M re-read the last row (or 16-row tile) and are never stored.
+  uint32_t arow[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) arow[i] = (uint32_t)min(m0 + 16 * i + r, p.M - 1);
+
+  // Scales first (the k-block loop waits on loads in issue order).
+  v4f sa[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) sa[i] = *reinterpret_cast<const v4f*>(p.as + (int64_t)arow[i] * KB + kb0);
+  // Raw weight-scale bits: converting them here would wait for the loads
+  // before the weight slice is even requested.
+  uint32_t swraw[KBW][NT];
+#pragma unroll
+  for (int s = 0; s < KBW; ++s)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int64_t at = (int64_t)((n0 + 16 * j) / kBlock) * KB + kb0 + s;
+      if constexpr (SDT == AKAS_DTYPE_F32)
+        swraw[s][j] = reinterpret_cast<const uint32_t*>(p.ws)[at];
+      else
+        swraw[s][j] = reinterpret_cast<const uint16_t*>(p.ws)[at];
+    }
+
+  // The weight slice: load q brings rows 2q and 2q+1, 512 bytes each.
+  const int wl_row = lane >> 5, wl_chunk = lane & 31;
+  const uint8_t* wsrc = p.w + (int64_t)(n0 + wl_row) * p.K + (int64_t)kb0 * kBlock + 16 * wl_chunk;
+  u32x4 wl[BN / 2];
+#pragma unroll
+  for (int q = 0; q < BN / 2; ++q) wl[q] = *reinterpret_cast<const u32x4*>(wsrc + (int64_t)(2 * q) * p.K);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // The first PF activation k-blocks.
+  const int lr = lane >> 2, lc = lane & 3;
+  const int sel = (4 * r + g) << 2;
+  const int last_tile = (p.M - 1) >> 4;
+  auto load_a = [&](int i, int s) -> RawFragment {
+    if constexpr (AF) {
+      const uint8_t* t = p.a + (((int64_t)min((m0 >> 4) + i, last_tile) * KB + kb0 + s) << 11) + 16 * lane;
+      return {*reinterpret_cast<const u32x4*>(t), *reinterpret_cast<const u32x4*>(t + 1024)};
+    } else {
+      const int row = min(m0 + 16 * i + lr, p.M - 1);
+      return load_raw_fragment(p.a + (int64_t)row * p.K + (int64_t)(kb0 + s) * kBlock, lc);
+    }
+  };
+  RawFragment araw[PF][MT];
+#pragma unroll
+  for (int s = 0; s < PF; ++s)
+#pragma unroll
+    for (int i = 0; i < MT; ++i) araw[s][i] = load_a(i, s);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Weight slice into LDS: row rho, chunk c at rho*512 + 16*(c ^ (rho & 15)),
+  // so the sixteen rows of a fragment read hit sixteen different banks.
+#pragma unroll
+  for (int q = 0; q < BN / 2; ++q) {
+    const int rho = 2 * q + wl_row;
+    *reinterpret_cast<u32x4*>(wlds + rho * WROW + 16 * (wl_chunk ^ (rho & 15))) = wl[q];
+  }
+
+  float sw[KBW][NT];
+#pragma unroll
+  for (int s = 0; s < KBW; ++s)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      sw[s][j] = __uint_as_float(SDT == AKAS_DTYPE_F32 ? swraw[s][j] : swraw[s][j] << 16);
+
+  v4f acc[MT][NT];
+#pragma unroll
+  for (int s = 0; s < KBW; ++s) {
+    const int slot = s % PF;
+    v8i af[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) af[i] = AF ? as_fragment(araw[slot][i]) : to_mfma_order(araw[slot][i], sel);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const uint8_t* wr = wlds + (16 * j + r) * WROW;
+      RawFragment wfr;
+      wfr.lo = *reinterpret_cast<const u32x4*>(wr + 16 * ((8 * s + g) ^ r));
+      wfr.hi = *reinterpret_cast<const u32x4*>(wr + 16 * ((8 * s + 4 + g) ^ r));
+      const v8i wf = as_fragment(wfr);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const v4f d = mfma_e4m3(wf, af[i]);
+        const float c = sa[i][s] * sw[s][j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[i][j][e] = s == 0 ? d[e] * c : __builtin_fmaf(d[e], c, acc[i][j][e]);
+      }
+    }
+    if (s + PF < KBW) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) araw[slot][i] = load_a(i, s + PF);
+    }
+  }
+
+  // Tile t = i*NT + j is summed and stored by wave t % 4, in wave order.
+  // Each wave writes its partials over its own (finished) weight slice.
+  v4f* red = reinterpret_cast<v4f*>(lds);
+  constexpr int RSTRIDE = WAVE_LDS / 16;
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      if ((i * NT + j) % kSplitWaves != wave) red[wave * RSTRIDE + (i * NT + j) * kWave + lane] = acc[i][j];
+  __syncthreads();
+  const int64_t obase = (int64_t)part * p.part_stride;
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int t = i * NT + j;
+      if (t % kSplitWaves != wave) continue;
+      v4f sum = wave == 0 ? acc[i][j] : red[t * kWave + lane];
+#pragma unroll
+      for (int w = 1; w < kSplitWaves; ++w) sum += w == wave ? acc[i][j] : red[w * RSTRIDE + t * kWave + lane];
+      const int row = m0 + 16 * i + r;
+      if (row < p.M) store_out4<OUT>(p.out, obase + (int64_t)row * p.ldo + n0 + 16 * j + 4 * g, sum);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Prefill GEMM: 256x256 tiles streamed into LDS by the gfx950 copy engine
 // (tile engine in gemm_dma.h).  N must be a multiple of 128 so that each
 // wave's 128 output columns are either all inside the matrix or all outside;
@@ -497,6 +716,41 @@ static bool dma_fits(const DenseArgs& a, int parts) {
          (a.part_stride * esz) % 16 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0;
 }
 
+// The split kernel: 2048-deep partitions, N a multiple of its 48-column
+// tiles, aligned 4-element output vectors and activation-scale vectors,
+// 32-bit code offsets.
+constexpr int kSplitNt = 3;
+static bool split_fits(const DenseArgs& a) {
+  const int esz = a.out_dtype == AKAS_DTYPE_F32 ? 4 : 2;
+  return a.kb_per_part == kSplitWaves * kSplitKbw && a.N % (16 * kSplitNt) == 0 &&
+         (int64_t)a.M * a.K < (1ll << 31) && (a.K / kBlock) % 4 == 0 && a.ldo % 4 == 0 &&
+         a.part_stride % 4 == 0 && reinterpret_cast<uintptr_t>(a.out) % (4 * esz) == 0 &&
+         reinterpret_cast<uintptr_t>(a.as) % 16 == 0;
+}
+
+static bool split_applies(const DenseArgs& a, int parts) {
+  return a.M > 16 && a.M <= 256 && split_fits(a) && parts >= 1;
+}
+
+template <int MT, int PF, int AF, int OUT, int SDT>
+static void launch_split(const DenseArgs& a, int parts, hipStream_t s) {
+  const int tiles = ((a.M + 16 * MT - 1) / (16 * MT)) * (a.N / (16 * kSplitNt));
+  dense_split_kernel<MT, kSplitNt, PF, AF, OUT, SDT><<<dim3(tiles, parts), 64 * kSplitWaves, 0, s>>>(a);
+}
+
+// Row tiles of the split kernel by M (16 < M <= 256).
+template <int AF, int OUT, int SDT>
+static void launch_split_m(const DenseArgs& a, int parts, hipStream_t s) {
+  if (a.M <= 32)
+    launch_split<1, 4, AF, OUT, SDT>(a, parts, s);
+  else if (a.M <= 64)
+    launch_split<2, 4, AF, OUT, SDT>(a, parts, s);
+  else if (a.M <= 128)
+    launch_split<4, 4, AF, OUT, SDT>(a, parts, s);
+  else
+    launch_split<8, 2, AF, OUT, SDT>(a, parts, s);
+}
+
 template <int OUT, int SDT>
 static void launch_dma(const DenseArgs& a, int parts, hipStream_t s) {
   const int tiles = ((a.M + dma::BM - 1) / dma::BM) * ((a.N + dma::BN - 1) / dma::BN);
@@ -541,6 +795,10 @@ static bool launch_wide(const DenseArgs& a, int parts, hipStream_t s) {
 template <int OUT, int SDT>
 static void launch_dense_t(const DenseArgs& a, int parts, hipStream_t s) {
   bool done = false;
+  if (split_applies(a, parts)) {
+    launch_split_m<0, OUT, SDT>(a, parts, s);
+    return;
+  }
   if (a.M <= 16)
     done = launch_wide<1, 2, 8, OUT, SDT>(a, parts, s);
   else if (a.M <= 32)
@@ -577,6 +835,24 @@ static void launch_dense_o(const DenseArgs& a, int parts, hipStream_t s) {
     launch_dense_t<OUT, AKAS_DTYPE_F32>(a, parts, s);
   else
     launch_dense_t<OUT, AKAS_DTYPE_BF16>(a, parts, s);
+}
+
+// fp8_linear's split-kernel path: activations quantized fragment-major.
+template <int OUT>
+static void launch_split_frag_o(const DenseArgs& a, hipStream_t s) {
+  if (a.ws_dtype == AKAS_DTYPE_F32)
+    launch_split_m<1, OUT, AKAS_DTYPE_F32>(a, 1, s);
+  else
+    launch_split_m<1, OUT, AKAS_DTYPE_BF16>(a, 1, s);
+}
+
+static int launch_split_frag(const DenseArgs& a, hipStream_t s) {
+  switch (a.out_dtype) {
+    case AKAS_DTYPE_F32: launch_split_frag_o<AKAS_DTYPE_F32>(a, s); break;
+    case AKAS_DTYPE_BF16: launch_split_frag_o<AKAS_DTYPE_BF16>(a, s); break;
+    default: launch_split_frag_o<AKAS_DTYPE_F16>(a, s);
+  }
+  return hipGetLastError() == hipSuccess ? AKAS_OK : AKAS_ERR_LAUNCH;
 }
 
 int launch_dense(const DenseArgs& a, int parts, hipStream_t s) {
@@ -638,7 +914,8 @@ using namespace akas;
 extern "C" size_t akas_fp8_linear_workspace_size(int64_t r, int64_t k, int64_t o) {
   (void)o;
   if (r <= 0 || k <= 0) return 0;
-  return align256((size_t)r * k) + align256((size_t)r * (k / kBlock) * sizeof(float));
+  // codes: rows rounded up to the 16-row tiles of the fragment-major layout
+  return align256((size_t)((r + 15) & ~15ll) * k) + align256((size_t)r * (k / kBlock) * sizeof(float));
 }
 
 extern "C" int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const void* w_scales,
@@ -663,12 +940,13 @@ extern "C" int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, con
       return hipGetLastError() == hipSuccess ? AKAS_OK : AKAS_ERR_LAUNCH;
   }
   uint8_t* codes = reinterpret_cast<uint8_t*>(workspace);
-  float* scales = reinterpret_cast<float*>(codes + align256((size_t)r * k));
-  int st = akas_quantize(x, x_dtype, codes, scales, r, k, stream);
-  if (st != AKAS_OK) return st;
+  float* scales = reinterpret_cast<float*>(codes + align256((size_t)((r + 15) & ~15ll) * k));
   DenseArgs a{codes, scales, w, w_scales, out, o, 0, (int)r, (int)o, (int)k,
               (int)(k / kBlock), scale_dtype, out_dtype, nullptr, 0};
-  return launch_dense(a, 1, s);
+  const bool frag = split_applies(a, 1);
+  const int st = launch_quantize(x, x_dtype, codes, scales, r, k, frag, s);
+  if (st != AKAS_OK) return st;
+  return frag ? launch_split_frag(a, s) : launch_dense(a, 1, s);
 }
 
 extern "C" int akas_projection_partial(const uint8_t* x, const float* activation_scales,

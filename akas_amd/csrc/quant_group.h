@@ -47,4 +47,10 @@ AKAS_DEV uint2 quantize8(const float v[8], float& scale) {
                     e4m3_encode4_scaled(v[4], v[5], v[6], v[7], gs));
 }
 
+// Activation quantizer launch (quantize.hip): row-major codes [rows, k], or
+// the fragment-major tiles of the decode GEMM when fragment_major is set
+// (rows rounded up to 16; the padding rows of the last tile are not written).
+int launch_quantize(const void* x, int x_dtype, uint8_t* out, float* scales, int64_t rows,
+                    int64_t k, bool fragment_major, hipStream_t s);
+
 }  // namespace akas

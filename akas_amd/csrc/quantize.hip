@@ -13,11 +13,17 @@ namespace akas {
 
 // One 128-group per 16 lanes; grid-stride over all groups.
 // (src/akas/quantization/activations/fp8/cuda.py:10-56, warp form :80-141)
-template <int DT>
+//
+// FRAG selects the fragment-major code layout that the decode GEMM reads:
+// the codes of rows 16t..16t+15, k-block b form one 2 KB tile at
+// (t * KB + b) * 2048, in which MFMA lane l = r + 16g (row r) finds chunks g
+// and 4+g of its row (16 bytes each) at 16l and 1024 + 16l, so one
+// contiguous 1 KB load per half delivers a whole operand fragment.
+template <int DT, bool FRAG>
 __global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ x,
                                                        uint8_t* __restrict__ out,
                                                        float* __restrict__ scales,
-                                                       int64_t groups) {
+                                                       int64_t groups, int kb_per_row) {
   const int lane16 = threadIdx.x & 15;
   const int64_t first = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
   const int64_t stride = ((int64_t)gridDim.x * blockDim.x) >> 4;
@@ -25,7 +31,15 @@ __global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ 
     const int64_t base = g * kBlock + lane16 * 8;
     float v[8], s;
     load8<DT>(x, base, v);
-    *reinterpret_cast<uint2*>(out + base) = quantize8(v, s);
+    const uint2 codes = quantize8(v, s);
+    int64_t at = base;
+    if constexpr (FRAG) {
+      const int64_t row = g / kb_per_row, kb = g - row * kb_per_row;
+      const int c = lane16 >> 1, r = (int)(row & 15);
+      at = (((row >> 4) * kb_per_row + kb) << 11) + ((c >> 2) << 10) + ((r + 16 * (c & 3)) << 4) +
+           8 * (lane16 & 1);
+    }
+    *reinterpret_cast<uint2*>(out + at) = codes;
     if (lane16 == 0) scales[g] = s;
   }
 }
@@ -88,7 +102,39 @@ static inline bool float_dtype(int d) {
 
 }  // namespace akas
 
+
 using namespace akas;
+
+namespace akas {
+
+template <bool FRAG>
+static void launch_quantize_t(const void* x, int x_dtype, uint8_t* out, float* scales,
+                              int64_t groups, int kb_per_row, hipStream_t s) {
+  const int64_t want = (groups + 15) / 16;  // 16 groups per 256-thread block
+  const int grid = (int)(want < 8192 ? want : 8192);
+  switch (x_dtype) {
+    case AKAS_DTYPE_F32:
+      quantize_kernel<AKAS_DTYPE_F32, FRAG><<<grid, 256, 0, s>>>(x, out, scales, groups, kb_per_row);
+      break;
+    case AKAS_DTYPE_F16:
+      quantize_kernel<AKAS_DTYPE_F16, FRAG><<<grid, 256, 0, s>>>(x, out, scales, groups, kb_per_row);
+      break;
+    default:
+      quantize_kernel<AKAS_DTYPE_BF16, FRAG><<<grid, 256, 0, s>>>(x, out, scales, groups, kb_per_row);
+  }
+}
+
+int launch_quantize(const void* x, int x_dtype, uint8_t* out, float* scales, int64_t rows,
+                    int64_t k, bool fragment_major, hipStream_t s) {
+  const int64_t groups = rows * (k / kBlock);
+  if (fragment_major)
+    launch_quantize_t<true>(x, x_dtype, out, scales, groups, (int)(k / kBlock), s);
+  else
+    launch_quantize_t<false>(x, x_dtype, out, scales, groups, (int)(k / kBlock), s);
+  return hipGetLastError() == hipSuccess ? AKAS_OK : AKAS_ERR_LAUNCH;
+}
+
+}  // namespace akas
 
 extern "C" int akas_quantize(const void* x, int x_dtype, uint8_t* out, float* scales,
                              int64_t rows, int64_t k, void* stream) {
@@ -96,22 +142,7 @@ extern "C" int akas_quantize(const void* x, int x_dtype, uint8_t* out, float* sc
   if (!float_dtype(x_dtype)) return AKAS_ERR_DTYPE;
   if (rows == 0) return AKAS_OK;
   if (!x || !out || !scales) return AKAS_ERR_NULL;
-  const int64_t groups = rows * (k / kBlock);
-  const int64_t want = (groups + 15) / 16;  // 16 groups per 256-thread block
-  const int grid = (int)(want < 8192 ? want : 8192);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  switch (x_dtype) {
-    case AKAS_DTYPE_F32:
-      quantize_kernel<AKAS_DTYPE_F32><<<grid, 256, 0, s>>>(x, out, scales, groups);
-      break;
-    case AKAS_DTYPE_F16:
-      quantize_kernel<AKAS_DTYPE_F16><<<grid, 256, 0, s>>>(x, out, scales, groups);
-      break;
-    default:
-      quantize_kernel<AKAS_DTYPE_BF16><<<grid, 256, 0, s>>>(x, out, scales, groups);
-  }
-  AKAS_CHECK_LAUNCH();
-  return AKAS_OK;
+  return launch_quantize(x, x_dtype, out, scales, rows, k, false, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int akas_dequantize_fp8(const uint8_t* codes, const float* scales, void* out,

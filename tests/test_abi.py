@@ -63,3 +63,5 @@ def test_workspace_size_formula():
     lib = _lib.load()
     assert lib.akas_fp8_linear_workspace_size(16, 2048, 6144) == 16 * 2048 + 16 * 16 * 4
     assert lib.akas_fp8_linear_workspace_size(0, 2048, 6144) == 0
+    # codes take whole 16-row tiles (the decode GEMM's fragment-major layout)
+    assert lib.akas_fp8_linear_workspace_size(17, 2048, 6144) == 32 * 2048 + 17 * 16 * 4 + 192

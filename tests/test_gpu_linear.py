@@ -42,7 +42,19 @@ def test_projection_exact_products(dev, m, k, n):
     np.testing.assert_array_equal(out.cpu().numpy(), exp)
 
 
-@pytest.mark.parametrize("m,k,n", EXACT_CASES[:6])
+# 2048-deep products with 16 < M <= 256 (the weight-stationary split-K
+# kernel): ragged M, 48-column tiles that straddle 128-column scale blocks
+# (N = 240, 480), and every m-tile height.
+SPLIT_CASES = [(17, 2048, 96), (40, 2048, 480), (64, 2048, 144), (100, 2048, 240),
+               (129, 2048, 192), (256, 2048, 336)]
+
+
+@pytest.mark.parametrize("m,k,n", SPLIT_CASES)
+def test_projection_exact_products_split(dev, m, k, n):
+    test_projection_exact_products(dev, m, k, n)
+
+
+@pytest.mark.parametrize("m,k,n", EXACT_CASES[:6] + SPLIT_CASES)
 def test_projection_varying_scales(dev, m, k, n):
     """Distinct per-row / per-block scales catch a wrong scale index."""
     import torch
@@ -82,12 +94,13 @@ def test_fp8_linear_decode_shapes(dev, m, scale_dtype):
     assert err < 1e-4, err
 
 
-@pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64])
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64, 100, 129, 256])
 @pytest.mark.parametrize("x_dtype", ["float32", "float16", "bfloat16"])
 def test_fp8_linear_fused_quantize_matches_two_step(dev, m, x_dtype):
-    """Up to 64 rows fp8_linear quantizes x inside the GEMM; the result is bit
-    for bit quantize -> projection_partial, and the in-kernel codes equal
-    the standalone quantizer's (stress rows included)."""
+    """fp8_linear quantizes x inside the GEMM (up to 8 rows) or into
+    fragment-major tiles (17-256 rows); either way the result is bit for bit
+    quantize -> projection_partial on row-major codes, and those codes equal
+    the oracle's (stress rows included)."""
     import torch
     from akas_amd import ops
     from golden_inputs import stress_rows
@@ -144,6 +157,29 @@ def test_fp8_linear_prefill_shapes(dev, m, k, n):
     assert rel_fro(got, exp) < 4e-3
 
 
+@pytest.mark.parametrize("m,n", [(40, 480), (256, 96)])
+@pytest.mark.parametrize("out_dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("scale_dtype", ["float32", "bfloat16"])
+def test_projection_split_out_and_scale_dtypes(dev, m, n, out_dtype, scale_dtype):
+    """16-bit outputs of exact products: the device rounding of each exact
+    sum equals the oracle's round-to-nearest-even, element for element."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(m + n)
+    k = 2048
+    x = exact_codes(rng, (m, k))
+    w = exact_codes(rng, (n, k))
+    xs = (2.0 ** rng.integers(-6, 2, (m, k // 128))).astype(np.float32)
+    ws = (2.0 ** rng.integers(-6, 2, ((n + 127) // 128, k // 128))).astype(np.float32)
+    out = ops.projection_partial(_t(x, dev), _t(xs, dev), _t(w, dev),
+                                 _t(ws, dev, getattr(torch, scale_dtype)),
+                                 out_dtype=getattr(torch, out_dtype))
+    torch.cuda.synchronize()
+    exp = ofp8.round_to(ofp8.fp8_linear(x, w, ws, activation_scales=xs), out_dtype)
+    np.testing.assert_array_equal(out.float().cpu().numpy(), exp)
+
+
 @pytest.mark.parametrize("parts", [2, 4])
 def test_projection_partitions_and_merge(dev, parts):
     import torch
@@ -162,6 +198,23 @@ def test_projection_partitions_and_merge(dev, parts):
     exp = ofp8.projection_partial(x, xs, w, ws, parts)
     np.testing.assert_array_equal(part.cpu().numpy(), exp)
     np.testing.assert_array_equal(merged.cpu().numpy(), ofp8.projection_merge(exp))
+
+
+def test_projection_split_partitions(dev):
+    """2048-deep partitions of a 4096-deep product run one split-K workgroup
+    grid per partition; each partition's tile lands at its own offset."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(5)
+    m, k, n = 40, 4096, 96
+    x = exact_codes(rng, (m, k))
+    w = exact_codes(rng, (n, k))
+    xs = (2.0 ** rng.integers(-6, 2, (m, k // 128))).astype(np.float32)
+    ws = (2.0 ** rng.integers(-6, 2, (1, k // 128))).astype(np.float32)
+    part = ops.projection_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev), partitions=2)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(part.cpu().numpy(), ofp8.projection_partial(x, xs, w, ws, 2))
 
 
 def test_linear_rejects_bad_geometry(dev):
