@@ -535,7 +535,7 @@ __global__ __launch_bounds__(256) void dense_small_kernel(DenseArgs p) {
 // Weights stream from HBM exactly once; activations are read from L2 once
 // per workgroup instead of once per wave.
 // ---------------------------------------------------------------------------
-constexpr int kWideBatch = 4;  // k-blocks of weights in flight per wave
+constexpr int kWideBatch = 2;  // k-blocks of weights in flight per wave
 
 template <int MT, int NTW, int KS>
 constexpr size_t wide_lds_bytes(int kbp) {
@@ -560,7 +560,7 @@ __global__ __launch_bounds__(64 * NTW * KS) void dense_wide_kernel(DenseArgs p) 
   const int kb0 = part * p.kb_per_part, kbp = p.kb_per_part;
   uint8_t* lds_a = smem;                                            // [kbp][ROWS][128]
   float* lds_s = reinterpret_cast<float*>(smem + (size_t)kbp * ROWS * 128);  // [kbp][ROWS]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nt = wave % NTW, ks = wave / NTW;
   const int n0 = blockIdx.x * (16 * NTW) + nt * 16;
   const int g = lane >> 4, r16 = lane & 15;
@@ -573,16 +573,31 @@ __global__ __launch_bounds__(64 * NTW * KS) void dense_wide_kernel(DenseArgs p) 
   auto issue = [&](int b) {
 #pragma unroll
     for (int j = 0; j < kWideBatch; ++j) {
-      const int lk = ks + KS * (b * kWideBatch + j);
-      if (lk < kbp) {
-        const int64_t ko = (int64_t)(kb0 + lk) * kBlock;
-        wl[j][0] = *reinterpret_cast<const u32x4*>(wrow + ko);
-        wl[j][1] = *reinterpret_cast<const u32x4*>(wrow + ko + 16);
-        wsv[j] = load_scale_t<SDT>(p.ws, ws_base + kb0 + lk);
-      }
+      // unconditional: a k-block past the partition re-reads its last one
+      // (never multiplied), so the compiler can wait for each load alone
+      const int lk = min(ks + KS * (b * kWideBatch + j), kbp - 1);
+      const int64_t ko = (int64_t)(kb0 + lk) * kBlock;
+      wl[j][0] = *reinterpret_cast<const u32x4*>(wrow + ko);
+      wl[j][1] = *reinterpret_cast<const u32x4*>(wrow + ko + 16);
+      wsv[j] = load_scale_t<SDT>(p.ws, ws_base + kb0 + lk);
     }
   };
+  // Fused quantize: the first pass of activation loads goes out before the
+  // weights, so quantizing waits only for them (loads complete in issue order).
+  constexpr int GPP = THREADS / 16, PASS = 4;
+  const int l16 = lane & 15, groups = QX ? p.M * kbp : 0;
+  Raw8 xraw[PASS];
+  if constexpr (QX != 0) {
+#pragma unroll
+    for (int u = 0; u < PASS; ++u) {
+      // unconditional (clamped) so the compiler can wait for each load alone
+      const int c = min((tid >> 4) + u * GPP, groups - 1);
+      xraw[u] = load8_raw<QX - 1>(p.x, (int64_t)(c / kbp) * p.K + (int64_t)(kb0 + c % kbp) * kBlock + l16 * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
   issue(0);
+  __builtin_amdgcn_sched_barrier(0);
 
   // 2. stage the activation slab (rows past M are zero) and its scales
   if constexpr (QX == 0) {
@@ -608,15 +623,18 @@ __global__ __launch_bounds__(64 * NTW * KS) void dense_wide_kernel(DenseArgs p) 
     // live groups (row, lk), one per 16 lanes, PASS groups per lane block with
     // all their loads issued before any is used; lane l16 holds values
     // 8*l16 .. 8*l16+7, i.e. half (l16 & 1) of chunk l16 / 2
-    constexpr int GPP = THREADS / 16, PASS = 4;
-    const int l16 = lane & 15, groups = p.M * kbp;
     for (int c0 = tid >> 4; c0 < groups; c0 += PASS * GPP) {
       float v[PASS][8];
+      const bool first = c0 == (tid >> 4);
 #pragma unroll
       for (int u = 0; u < PASS; ++u) {
         const int c = c0 + u * GPP;
-        if (c < groups)
-          load8<QX - 1>(p.x, (int64_t)(c / kbp) * p.K + (int64_t)(kb0 + c % kbp) * kBlock + l16 * 8, v[u]);
+        if (c < groups) {
+          if (first)
+            unpack8<QX - 1>(xraw[u], v[u]);
+          else
+            load8<QX - 1>(p.x, (int64_t)(c / kbp) * p.K + (int64_t)(kb0 + c % kbp) * kBlock + l16 * 8, v[u]);
+        }
       }
 #pragma unroll
       for (int u = 0; u < PASS; ++u) {
@@ -866,11 +884,12 @@ int launch_dense(const DenseArgs& a, int parts, hipStream_t s) {
 
 // Decode-sized fp8_linear in one launch: the wide kernel quantizes x while
 // staging it.  False when the shape does not fit the wide kernel.
-// Up to kFusedQuantizeRows rows: beyond that every workgroup re-quantizing
-// the whole slab costs more than the separate quantizer's launch (decode
-// sweep, K=2048, N=6144: fused 5.1 / 6.3 us vs 7.5 / 7.9 us at M=1 / 4, but
-// 9.2 vs 8.3 us at M=16).
-constexpr int kFusedQuantizeRows = 8;
+// Up to kFusedQuantizeRows rows (the wide kernel's one-tile slab): the x
+// loads go out ahead of the weights, so quantizing overlaps the weight
+// stream, and the launch saved outweighs every workgroup re-quantizing the
+// slab (K=2048, N=6144: fused 5.1 / 6.0 / 7.7 us vs 7.5 / 7.9 / 8.3 us
+// quantize + GEMM at M=1 / 4 / 16).  Larger batches use the split kernel.
+constexpr int kFusedQuantizeRows = 16;
 
 template <int OUT, int SDT, int QX>
 static bool launch_fused_small_t(const DenseArgs& a, hipStream_t s) {

@@ -32,6 +32,48 @@ AKAS_DEV void load8(const void* x, int64_t base, float v[8]) {
   }
 }
 
+// The same 8 values as raw bits, widened later by unpack8: a kernel can put
+// these loads in flight ahead of others and convert once they arrive.
+struct Raw8 {
+  u32x4 lo, hi;  // hi: second half of an f32 octet (unused for 16-bit dtypes)
+};
+
+template <int DT>
+AKAS_DEV Raw8 load8_raw(const void* x, int64_t base) {
+  Raw8 r;
+  if constexpr (DT == AKAS_DTYPE_F32) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(x) + base);
+    r.lo = p[0];
+    r.hi = p[1];
+  } else {
+    r.lo = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(x) + base);
+    r.hi = u32x4{0u, 0u, 0u, 0u};
+  }
+  return r;
+}
+
+template <int DT>
+AKAS_DEV void unpack8(const Raw8& r, float v[8]) {
+  if constexpr (DT == AKAS_DTYPE_F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = __uint_as_float(r.lo[i]);
+      v[4 + i] = __uint_as_float(r.hi[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (DT == AKAS_DTYPE_BF16) {
+        v[2 * i] = __uint_as_float(r.lo[i] << 16);
+        v[2 * i + 1] = __uint_as_float(r.lo[i] & 0xFFFF0000u);
+      } else {
+        v[2 * i] = f16_bits_to_f32(r.lo[i] & 0xFFFFu);
+        v[2 * i + 1] = f16_bits_to_f32(r.lo[i] >> 16);
+      }
+    }
+  }
+}
+
 // Codes of this lane's 8 values (low word = values 0..3) and the group scale
 // max(max|x|, 1e-12) / 448, the maximum taken over the 16 lanes of the group
 // (lanes 16*i .. 16*i+15 of the wave, all active).
