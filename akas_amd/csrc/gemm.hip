@@ -232,20 +232,30 @@ AKAS_DEV void store_out4(void* out, int64_t i, const v4f& v) {
   }
 }
 
-constexpr int kSplitWaves = 4;
-constexpr int kSplitKbw = 4;  // k-blocks per wave: 2048-deep partitions
+constexpr int kSplitQuarters = 4;  // k-split of a workgroup: four waves
+constexpr int kBufferDword3 = 0x00020000;  // buffer resource word 3 (raw 32-bit data)
+constexpr int kSplitKbw = 4;       // k-blocks per wave: 2048-deep partitions
 
-template <int MT, int NT, int PF, int AF, int OUT, int SDT>
-__global__ __launch_bounds__(64 * kSplitWaves) void dense_split_kernel(DenseArgs p) {
-  constexpr int KBW = kSplitKbw, BM = 16 * MT, BN = 16 * NT, TILES = MT * NT;
-  constexpr int WROW = KBW * kBlock;                 // bytes of a weight row per wave
-  constexpr int WAVE_LDS = BN * WROW > TILES * kWave * 16 ? BN * WROW : TILES * kWave * 16;
-  static_assert(PF >= 1 && PF <= KBW, "activation prefetch depth");
+// PF: activation k-blocks loaded up front (the rest follow the first
+// multiplies).  AFIRST: activation loads ahead of the weight loads (small
+// tiles, whose activations are quick to land) or right behind them (large
+// tiles: the weights' HBM latency goes first).
+template <int MT, int NT, int PF, int AFIRST, int AF, int OUT, int SDT>
+__global__ __launch_bounds__(64 * kSplitQuarters) void dense_split_kernel(DenseArgs p) {
+  constexpr int KBW = kSplitKbw, BM = 16 * MT, BN = 16 * NT;
+  constexpr int WT = MT * NT;                        // output tiles per wave
+  constexpr int WROW = KBW * kBlock;                 // bytes of a weight row per quarter
+  constexpr int QUARTER = BN * WROW;                 // LDS bytes of one quarter's slice
+  constexpr int RED = WT * kWave * 16;               // LDS bytes of one wave's partials
   static_assert(BN % 2 == 0 && WROW == 512, "two 512-byte weight rows per load");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kSplitWaves * WAVE_LDS];
+  static_assert(RED <= QUARTER, "a wave's partials overwrite its own weight slice");
+  static_assert(PF >= 1 && PF <= KBW, "activation prefetch depth");
+  constexpr int LDS_BYTES = kSplitQuarters * QUARTER;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
 
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kq = wave;
   const int tiles_m = (p.M + BM - 1) / BM, tiles_n = p.N / BN;
   // m-tiles of one column block are adjacent, so both reads of a weight
   // slice land in the same XCD's L2
@@ -254,8 +264,8 @@ __global__ __launch_bounds__(64 * kSplitWaves) void dense_split_kernel(DenseArgs
   const int m0 = tm * BM, n0 = tn * BN;
   const int KB = p.K / kBlock;
   const int part = blockIdx.y;
-  const int kb0 = part * p.kb_per_part + wave * KBW;
-  uint8_t* wlds = lds + wave * WAVE_LDS;
+  const int kb0 = part * p.kb_per_part + kq * KBW;
+  uint8_t* wq = lds + kq * QUARTER;  // this wave's weight slice
 
   // Rows past M re-read the last row (or 16-row tile) and are never stored.
   uint32_t arow[MT];
@@ -280,40 +290,63 @@ __global__ __launch_bounds__(64 * kSplitWaves) void dense_split_kernel(DenseArgs
         swraw[s][j] = reinterpret_cast<const uint16_t*>(p.ws)[at];
     }
 
-  // The weight slice: load q brings rows 2q and 2q+1, 512 bytes each.
-  const int wl_row = lane >> 5, wl_chunk = lane & 31;
-  const uint8_t* wsrc = p.w + (int64_t)(n0 + wl_row) * p.K + (int64_t)kb0 * kBlock + 16 * wl_chunk;
-  u32x4 wl[BN / 2];
-#pragma unroll
-  for (int q = 0; q < BN / 2; ++q) wl[q] = *reinterpret_cast<const u32x4*>(wsrc + (int64_t)(2 * q) * p.K);
-  __builtin_amdgcn_sched_barrier(0);
-
-  // The first PF activation k-blocks.
+  // Activation k-blocks of this quarter.
   const int lr = lane >> 2, lc = lane & 3;
   const int sel = (4 * r + g) << 2;
   const int last_tile = (p.M - 1) >> 4;
+  // Buffer loads: the tile offset of a fragment is wave-uniform (scalar),
+  // so a load costs one vector register of address for the whole wave.
+  const int a_bytes = AF ? ((p.M + 15) >> 4) * KB * 2048 : p.M * p.K;
+  const __amdgpu_buffer_rsrc_t a_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.a), (short)0, a_bytes, kBufferDword3);
   auto load_a = [&](int i, int s) -> RawFragment {
+    RawFragment f;
     if constexpr (AF) {
-      const uint8_t* t = p.a + (((int64_t)min((m0 >> 4) + i, last_tile) * KB + kb0 + s) << 11) + 16 * lane;
-      return {*reinterpret_cast<const u32x4*>(t), *reinterpret_cast<const u32x4*>(t + 1024)};
+      const int t = ((min((m0 >> 4) + i, last_tile) * KB + kb0 + s) << 11);
+      f.lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, 16 * lane, t, 0));
+      f.hi = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, 16 * lane, t + 1024, 0));
     } else {
       const int row = min(m0 + 16 * i + lr, p.M - 1);
-      return load_raw_fragment(p.a + (int64_t)row * p.K + (int64_t)(kb0 + s) * kBlock, lc);
+      const int off = row * p.K + (kb0 + s) * kBlock + 16 * lc;
+      f.lo = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0));
+      f.hi = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off + 64, 0, 0));
     }
+    return f;
   };
   RawFragment araw[PF][MT];
+  auto issue_a = [&]() {
 #pragma unroll
-  for (int s = 0; s < PF; ++s)
+    for (int s = 0; s < PF; ++s)
 #pragma unroll
-    for (int i = 0; i < MT; ++i) araw[s][i] = load_a(i, s);
+      for (int i = 0; i < MT; ++i) araw[s][i] = load_a(i, s);
+  };
+
+  // The wave's weight slice, two rows of 512 contiguous bytes per load.
+  constexpr int WLOADS = BN / 2;
+  const int wl_row = lane >> 5, wl_chunk = lane & 31;
+  const uint8_t* wsrc = p.w + (int64_t)(n0 + wl_row) * p.K + (int64_t)kb0 * kBlock + 16 * wl_chunk;
+  u32x4 wl[WLOADS];
+  auto issue_w = [&]() {
+#pragma unroll
+    for (int q = 0; q < WLOADS; ++q) wl[q] = *reinterpret_cast<const u32x4*>(wsrc + (int64_t)(2 * q) * p.K);
+  };
+  if constexpr (AFIRST) {
+    issue_a();
+    __builtin_amdgcn_sched_barrier(0);
+    issue_w();
+  } else {
+    issue_w();
+    __builtin_amdgcn_sched_barrier(0);
+    issue_a();
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // Weight slice into LDS: row rho, chunk c at rho*512 + 16*(c ^ (rho & 15)),
   // so the sixteen rows of a fragment read hit sixteen different banks.
 #pragma unroll
-  for (int q = 0; q < BN / 2; ++q) {
+  for (int q = 0; q < WLOADS; ++q) {
     const int rho = 2 * q + wl_row;
-    *reinterpret_cast<u32x4*>(wlds + rho * WROW + 16 * (wl_chunk ^ (rho & 15))) = wl[q];
+    *reinterpret_cast<u32x4*>(wq + rho * WROW + 16 * (wl_chunk ^ (rho & 15))) = wl[q];
   }
 
   float sw[KBW][NT];
@@ -330,36 +363,43 @@ __global__ __launch_bounds__(64 * kSplitWaves) void dense_split_kernel(DenseArgs
     v8i af[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) af[i] = AF ? as_fragment(araw[slot][i]) : to_mfma_order(araw[slot][i], sel);
+    if (s + PF < KBW) {
+      // refill this slot once its fragments are taken (not hoisted, which
+      // would hold every k-block in registers at once)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) araw[slot][i] = load_a(i, s + PF);
+    }
+    v8i wf[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      const uint8_t* wr = wlds + (16 * j + r) * WROW;
+      const uint8_t* wr = wq + (16 * j + r) * WROW;
       RawFragment wfr;
       wfr.lo = *reinterpret_cast<const u32x4*>(wr + 16 * ((8 * s + g) ^ r));
       wfr.hi = *reinterpret_cast<const u32x4*>(wr + 16 * ((8 * s + 4 + g) ^ r));
-      const v8i wf = as_fragment(wfr);
+      wf[j] = as_fragment(wfr);
+    }
+    // m-tile by m-tile, so only one m-tile's products wait for their scale fold
 #pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const v4f d = mfma_e4m3(wf, af[i]);
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const v4f d = mfma_e4m3(wf[j], af[i]);
         const float c = sa[i][s] * sw[s][j];
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[i][j][e] = s == 0 ? d[e] * c : __builtin_fmaf(d[e], c, acc[i][j][e]);
       }
-    }
-    if (s + PF < KBW) {
-#pragma unroll
-      for (int i = 0; i < MT; ++i) araw[slot][i] = load_a(i, s + PF);
-    }
   }
 
   // Tile t = i*NT + j is summed and stored by wave t % 4, in wave order.
   // Each wave writes its partials over its own (finished) weight slice.
   v4f* red = reinterpret_cast<v4f*>(lds);
-  constexpr int RSTRIDE = WAVE_LDS / 16;
+  auto slot = [&](int q, int t) { return q * (QUARTER / 16) + t * kWave + lane; };
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
     for (int j = 0; j < NT; ++j)
-      if ((i * NT + j) % kSplitWaves != wave) red[wave * RSTRIDE + (i * NT + j) * kWave + lane] = acc[i][j];
+      if ((i * NT + j) % kSplitQuarters != kq) red[slot(kq, i * NT + j)] = acc[i][j];
   __syncthreads();
   const int64_t obase = (int64_t)part * p.part_stride;
 #pragma unroll
@@ -367,10 +407,10 @@ __global__ __launch_bounds__(64 * kSplitWaves) void dense_split_kernel(DenseArgs
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const int t = i * NT + j;
-      if (t % kSplitWaves != wave) continue;
-      v4f sum = wave == 0 ? acc[i][j] : red[t * kWave + lane];
+      if (t % kSplitQuarters != kq) continue;
+      v4f sum = kq == 0 ? acc[i][j] : red[slot(0, t)];
 #pragma unroll
-      for (int w = 1; w < kSplitWaves; ++w) sum += w == wave ? acc[i][j] : red[w * RSTRIDE + t * kWave + lane];
+      for (int q = 1; q < kSplitQuarters; ++q) sum += q == kq ? acc[i][j] : red[slot(q, t)];
       const int row = m0 + 16 * i + r;
       if (row < p.M) store_out4<OUT>(p.out, obase + (int64_t)row * p.ldo + n0 + 16 * j + 4 * g, sum);
     }
@@ -740,7 +780,7 @@ static bool dma_fits(const DenseArgs& a, int parts) {
 constexpr int kSplitNt = 3;
 static bool split_fits(const DenseArgs& a) {
   const int esz = a.out_dtype == AKAS_DTYPE_F32 ? 4 : 2;
-  return a.kb_per_part == kSplitWaves * kSplitKbw && a.N % (16 * kSplitNt) == 0 &&
+  return a.kb_per_part == kSplitQuarters * kSplitKbw && a.N % (16 * kSplitNt) == 0 &&
          (int64_t)a.M * a.K < (1ll << 31) && (a.K / kBlock) % 4 == 0 && a.ldo % 4 == 0 &&
          a.part_stride % 4 == 0 && reinterpret_cast<uintptr_t>(a.out) % (4 * esz) == 0 &&
          reinterpret_cast<uintptr_t>(a.as) % 16 == 0;
@@ -750,23 +790,25 @@ static bool split_applies(const DenseArgs& a, int parts) {
   return a.M > 16 && a.M <= 256 && split_fits(a) && parts >= 1;
 }
 
-template <int MT, int PF, int AF, int OUT, int SDT>
+template <int MT, int PF, int AFIRST, int AF, int OUT, int SDT>
 static void launch_split(const DenseArgs& a, int parts, hipStream_t s) {
   const int tiles = ((a.M + 16 * MT - 1) / (16 * MT)) * (a.N / (16 * kSplitNt));
-  dense_split_kernel<MT, kSplitNt, PF, AF, OUT, SDT><<<dim3(tiles, parts), 64 * kSplitWaves, 0, s>>>(a);
+  dense_split_kernel<MT, kSplitNt, PF, AFIRST, AF, OUT, SDT>
+      <<<dim3(tiles, parts), 64 * kSplitQuarters, 0, s>>>(a);
 }
 
-// Row tiles of the split kernel by M (16 < M <= 256).
+// Row tiles of the split kernel by M (16 < M <= 256), two tiles per column
+// block so that the grid covers 256 CUs at N = 6144.
 template <int AF, int OUT, int SDT>
 static void launch_split_m(const DenseArgs& a, int parts, hipStream_t s) {
   if (a.M <= 32)
-    launch_split<1, 4, AF, OUT, SDT>(a, parts, s);
+    launch_split<1, 4, 1, AF, OUT, SDT>(a, parts, s);
   else if (a.M <= 64)
-    launch_split<2, 4, AF, OUT, SDT>(a, parts, s);
+    launch_split<2, 4, 1, AF, OUT, SDT>(a, parts, s);
   else if (a.M <= 128)
-    launch_split<4, 4, AF, OUT, SDT>(a, parts, s);
+    launch_split<4, 4, 1, AF, OUT, SDT>(a, parts, s);
   else
-    launch_split<8, 2, AF, OUT, SDT>(a, parts, s);
+    launch_split<8, 2, 0, AF, OUT, SDT>(a, parts, s);
 }
 
 template <int OUT, int SDT>
