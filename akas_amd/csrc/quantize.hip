@@ -18,29 +18,36 @@ namespace akas {
 // the codes of rows 16t..16t+15, k-block b form one 2 KB tile at
 // (t * KB + b) * 2048, in which MFMA lane l = r + 16g (row r) finds chunks g
 // and 4+g of its row (16 bytes each) at 16l and 1024 + 16l, so one
-// contiguous 1 KB load per half delivers a whole operand fragment.
+// contiguous 1 KB load per half delivers a whole operand fragment.  Groups
+// are then taken tile by tile (16 rows of one k-block per 256 threads), so
+// a block writes one whole tile; the padding rows of the last tile are
+// skipped.
 template <int DT, bool FRAG>
 __global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ x,
                                                        uint8_t* __restrict__ out,
                                                        float* __restrict__ scales,
-                                                       int64_t groups, int kb_per_row) {
+                                                       int64_t groups, int kb_per_row, int64_t rows) {
   const int lane16 = threadIdx.x & 15;
   const int64_t first = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
   const int64_t stride = ((int64_t)gridDim.x * blockDim.x) >> 4;
   for (int64_t g = first; g < groups; g += stride) {
-    const int64_t base = g * kBlock + lane16 * 8;
+    int64_t gi = g, at;                         // gi: the group in row-major order
+    if constexpr (FRAG) {
+      const int64_t t = g >> 4;                 // tile (16-row block, k-block)
+      const int64_t kb = t % kb_per_row, rb = t / kb_per_row;
+      const int r = (int)(g & 15), c = lane16 >> 1;
+      const int64_t row = rb * 16 + r;
+      if (row >= rows) continue;                // uniform across the group's 16 lanes
+      gi = row * kb_per_row + kb;
+      at = ((rb * kb_per_row + kb) << 11) + ((c >> 2) << 10) + ((r + 16 * (c & 3)) << 4) + 8 * (lane16 & 1);
+    }
+    const int64_t base = gi * kBlock + lane16 * 8;
+    if constexpr (!FRAG) at = base;
     float v[8], s;
     load8<DT>(x, base, v);
     const uint2 codes = quantize8(v, s);
-    int64_t at = base;
-    if constexpr (FRAG) {
-      const int64_t row = g / kb_per_row, kb = g - row * kb_per_row;
-      const int c = lane16 >> 1, r = (int)(row & 15);
-      at = (((row >> 4) * kb_per_row + kb) << 11) + ((c >> 2) << 10) + ((r + 16 * (c & 3)) << 4) +
-           8 * (lane16 & 1);
-    }
     *reinterpret_cast<uint2*>(out + at) = codes;
-    if (lane16 == 0) scales[g] = s;
+    if (lane16 == 0) scales[gi] = s;
   }
 }
 
@@ -109,28 +116,28 @@ namespace akas {
 
 template <bool FRAG>
 static void launch_quantize_t(const void* x, int x_dtype, uint8_t* out, float* scales,
-                              int64_t groups, int kb_per_row, hipStream_t s) {
+                              int64_t groups, int kb_per_row, int64_t rows, hipStream_t s) {
   const int64_t want = (groups + 15) / 16;  // 16 groups per 256-thread block
   const int grid = (int)(want < 8192 ? want : 8192);
   switch (x_dtype) {
     case AKAS_DTYPE_F32:
-      quantize_kernel<AKAS_DTYPE_F32, FRAG><<<grid, 256, 0, s>>>(x, out, scales, groups, kb_per_row);
+      quantize_kernel<AKAS_DTYPE_F32, FRAG><<<grid, 256, 0, s>>>(x, out, scales, groups, kb_per_row, rows);
       break;
     case AKAS_DTYPE_F16:
-      quantize_kernel<AKAS_DTYPE_F16, FRAG><<<grid, 256, 0, s>>>(x, out, scales, groups, kb_per_row);
+      quantize_kernel<AKAS_DTYPE_F16, FRAG><<<grid, 256, 0, s>>>(x, out, scales, groups, kb_per_row, rows);
       break;
     default:
-      quantize_kernel<AKAS_DTYPE_BF16, FRAG><<<grid, 256, 0, s>>>(x, out, scales, groups, kb_per_row);
+      quantize_kernel<AKAS_DTYPE_BF16, FRAG><<<grid, 256, 0, s>>>(x, out, scales, groups, kb_per_row, rows);
   }
 }
 
 int launch_quantize(const void* x, int x_dtype, uint8_t* out, float* scales, int64_t rows,
                     int64_t k, bool fragment_major, hipStream_t s) {
-  const int64_t groups = rows * (k / kBlock);
-  if (fragment_major)
-    launch_quantize_t<true>(x, x_dtype, out, scales, groups, (int)(k / kBlock), s);
+  const int kb = (int)(k / kBlock);
+  if (fragment_major)  // whole 16-row tiles, padding rows skipped
+    launch_quantize_t<true>(x, x_dtype, out, scales, ((rows + 15) / 16) * 16 * kb, kb, rows, s);
   else
-    launch_quantize_t<false>(x, x_dtype, out, scales, groups, (int)(k / kBlock), s);
+    launch_quantize_t<false>(x, x_dtype, out, scales, rows * kb, kb, rows, s);
   return hipGetLastError() == hipSuccess ? AKAS_OK : AKAS_ERR_LAUNCH;
 }
 
