@@ -16,6 +16,7 @@
 // expert_partial x2 -> swiglu_experts -> quantize.
 #include "gemm_core.h"
 #include "gemm_dma.h"
+#include "quant_group.h"
 
 namespace akas {
 
@@ -231,10 +232,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
-        float m = rmax[i][e4];
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o, 16));
-        rmax[i][e4] = m;
+        rmax[i][e4] = row16_max(rmax[i][e4]);
       }
     if ((lane & 15) == 0) {
 #pragma unroll

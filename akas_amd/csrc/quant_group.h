@@ -77,12 +77,28 @@ AKAS_DEV void unpack8(const Raw8& r, float v[8]) {
 // Codes of this lane's 8 values (low word = values 0..3) and the group scale
 // max(max|x|, 1e-12) / 448, the maximum taken over the 16 lanes of the group
 // (lanes 16*i .. 16*i+15 of the wave, all active).
+//
+// The 16-lane maximum is four DPP row operations (quad swaps, then the
+// half-row and row mirrors), which stay in the VALU instead of going
+// through the LDS crossbar as lane shuffles do.
+template <int CTRL>
+AKAS_DEV float dpp_max(float m) {
+  const float o = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), CTRL, 0xF, 0xF, true));
+  return __builtin_fmaxf(m, o);
+}
+
+AKAS_DEV float row16_max(float m) {
+  m = dpp_max<0xB1>(m);   // quad_perm [1,0,3,2]: lane ^ 1
+  m = dpp_max<0x4E>(m);   // quad_perm [2,3,0,1]: lane ^ 2
+  m = dpp_max<0x141>(m);  // row_half_mirror: lane i <- 7 - i within 8 lanes
+  return dpp_max<0x140>(m);  // row_mirror: lane i <- 15 - i within 16 lanes
+}
+
 AKAS_DEV uint2 quantize8(const float v[8], float& scale) {
   float m = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(v[i]));
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o, 16));
+  m = row16_max(m);
   const GroupScale gs = make_group_scale(m);
   scale = gs.s;
   return make_uint2(e4m3_encode4_scaled(v[0], v[1], v[2], v[3], gs),

@@ -97,7 +97,7 @@ def test_fp8_linear_decode_shapes(dev, m, scale_dtype):
 @pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64, 100, 129, 256])
 @pytest.mark.parametrize("x_dtype", ["float32", "float16", "bfloat16"])
 def test_fp8_linear_fused_quantize_matches_two_step(dev, m, x_dtype):
-    """fp8_linear quantizes x inside the GEMM (up to 8 rows) or into
+    """fp8_linear quantizes x inside the GEMM (up to 16 rows) or into
     fragment-major tiles (17-256 rows); either way the result is bit for bit
     quantize -> projection_partial on row-major codes, and those codes equal
     the oracle's (stress rows included)."""
