@@ -43,6 +43,17 @@ class ExpertWeights:
         return self.w1.shape[1]
 
 
+_ACTIVE = {}
+
+
+def _all_active(rows, device):
+    """Cached all-ones activity mask (filled once per size and device)."""
+    key = (rows, str(device))
+    if key not in _ACTIVE:
+        _ACTIVE[key] = torch.ones(rows, dtype=torch.int32, device=device)
+    return _ACTIVE[key]
+
+
 def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
                router="biased_softmax_router", scale=1.0, normalize=True, fused_swiglu=True,
                packed=False, max_block_m=64, product_dtype=torch.float32,
@@ -56,7 +67,7 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
     rows, hidden = x.shape
     experts = weights.experts
     if active is None:
-        active = torch.ones(rows, dtype=torch.int32, device=x.device)
+        active = _all_active(rows, x.device)
     if router == "biased_router":
         ids, probability = ops.biased_router(logits, bias, top=top, scale=scale,
                                              normalize=normalize)
@@ -71,11 +82,20 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
     if packed:
         codes, scales, offsets = ops.expert_pack(codes, scales, counts, routes, tile_experts,
                                                  tile_rows, top=top, max_block_m=max_block_m)
+    # Intermediates are left unfilled: every entry a consumer reads is
+    # written -- active rows route all `top` ranks, the expert products read
+    # only routed entries and the combine skips inactive rows.
+    width = weights.width
     if fused_swiglu:
+        act_rows = ((ops.tile_capacity(rows, top, experts, max_block_m) * max_block_m,) if packed
+                    else (rows, top))
         act, act_scales = ops.fp8_expert_swiglu(
             codes, scales, weights.w1, weights.s1, weights.w3, weights.s3, counts, routes,
             tile_experts, tile_rows, offsets, product_dtype=product_dtype,
             activation_dtype=activation_dtype, packed_input=packed, packed_output=packed,
+            out=torch.empty((*act_rows, width), dtype=torch.uint8, device=x.device),
+            output_scales=torch.empty((*act_rows, width // ops.BLOCK), dtype=torch.float32,
+                                      device=x.device),
             **common)
     else:
         gate = ops.expert_partial(codes, scales, weights.w1, weights.s1, counts, routes,
@@ -87,6 +107,8 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
     contributions = ops.expert_partial(
         act, act_scales, weights.w2, weights.s2, counts, routes, tile_experts, tile_rows,
         offsets, routed_input=not packed, packed_input=packed, output_dtype=contribution_dtype,
+        out=torch.empty((rows, top, hidden), dtype=ops._torch_dtype(contribution_dtype),
+                        device=x.device),
         **common)
     out = ops.routed_combine(contributions, probability, active)
     if return_routing:
