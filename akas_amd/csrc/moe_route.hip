@@ -303,6 +303,60 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ e
     if (col + j < c) out[row * c + col + j] = acc[j];
 }
 
+// Eight consecutive columns per thread with 16-byte loads (two for f32
+// inputs), the loads of up to four ranks in flight before their folds; the
+// fold order (rank 0 first, one fma per rank) is the generic kernel's, so the
+// result is the same bit for bit.  c % 8 == 0 and 16-byte aligned rows.
+template <int DT>
+__global__ __launch_bounds__(256) void combine8_kernel(const void* __restrict__ experts,
+                                                       const float* __restrict__ weights,
+                                                       const int32_t* __restrict__ active,
+                                                       float* __restrict__ out, int top,
+                                                       int64_t c) {
+  const int64_t row = blockIdx.y;
+  const int64_t col = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (col >= c) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (!active || active[row] != 0) {
+    constexpr int U = 4;
+    for (int k0 = 0; k0 < top; k0 += U) {
+      u32x4 raw[U][DT == AKAS_DTYPE_F32 ? 2 : 1];
+      float wv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = min(k0 + u, top - 1);  // unconditional: a clamped rank is never folded
+        wv[u] = weights[row * top + k];
+        const int64_t base = (row * top + k) * c + col;
+        if constexpr (DT == AKAS_DTYPE_F32) {
+          const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(experts) + base);
+          raw[u][0] = src[0];
+          raw[u][1] = src[1];
+        } else {
+          raw[u][0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(experts) + base);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (k0 + u >= top) break;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float v;
+          if constexpr (DT == AKAS_DTYPE_F32)
+            v = __uint_as_float(raw[u][j >> 2][j & 3]);
+          else if constexpr (DT == AKAS_DTYPE_BF16)
+            v = bf16_bits_to_f32((raw[u][0][j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+          else
+            v = f16_bits_to_f32((raw[u][0][j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+          acc[j] = __builtin_fmaf(v, wv[u], acc[j]);
+        }
+      }
+    }
+  }
+  float4* dst = reinterpret_cast<float4*>(out + row * c + col);
+  dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+}
+
 static inline bool float_dtype(int d) {
   return d == AKAS_DTYPE_F32 || d == AKAS_DTYPE_F16 || d == AKAS_DTYPE_BF16;
 }
@@ -428,13 +482,25 @@ extern "C" int akas_routed_combine(const void* experts, int input_dtype, const f
   if (r == 0) return AKAS_OK;
   if (!experts || !weights || !out) return AKAS_ERR_NULL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const size_t esz = input_dtype == AKAS_DTYPE_F32 ? 4 : 2;
+  const bool vec = c % 8 == 0 && reinterpret_cast<uintptr_t>(experts) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % 16 == 0;
   for (int64_t r0 = 0; r0 < r; r0 += 65535) {
     const int64_t rr = r - r0 < 65535 ? r - r0 : 65535;
-    dim3 grid((unsigned)((c + 1023) / 1024), (unsigned)rr);
-    const size_t esz = input_dtype == AKAS_DTYPE_F32 ? 4 : 2;
-    combine_kernel<<<grid, 256, 0, s>>>(
-        reinterpret_cast<const char*>(experts) + r0 * top * c * esz, input_dtype,
-        weights + r0 * top, active ? active + r0 : nullptr, out + r0 * c, rr, top, c);
+    const char* ex = reinterpret_cast<const char*>(experts) + r0 * top * c * esz;
+    const int32_t* act = active ? active + r0 : nullptr;
+    if (vec) {
+      dim3 grid((unsigned)((c / 8 + 255) / 256), (unsigned)rr);
+      if (input_dtype == AKAS_DTYPE_F32)
+        combine8_kernel<AKAS_DTYPE_F32><<<grid, 256, 0, s>>>(ex, weights + r0 * top, act, out + r0 * c, top, c);
+      else if (input_dtype == AKAS_DTYPE_BF16)
+        combine8_kernel<AKAS_DTYPE_BF16><<<grid, 256, 0, s>>>(ex, weights + r0 * top, act, out + r0 * c, top, c);
+      else
+        combine8_kernel<AKAS_DTYPE_F16><<<grid, 256, 0, s>>>(ex, weights + r0 * top, act, out + r0 * c, top, c);
+    } else {
+      dim3 grid((unsigned)((c + 1023) / 1024), (unsigned)rr);
+      combine_kernel<<<grid, 256, 0, s>>>(ex, input_dtype, weights + r0 * top, act, out + r0 * c, rr, top, c);
+    }
   }
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;

@@ -395,16 +395,19 @@ def test_swiglu_wide_range_accuracy(dev):
     np.testing.assert_allclose(out, exact, rtol=2e-6, atol=1e-30)
 
 
-@pytest.mark.parametrize("in_dtype", ["float32", "bfloat16"])
-def test_routed_combine(dev, in_dtype):
+@pytest.mark.parametrize("in_dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("top,c", [(4, 2048), (6, 2048), (1, 24), (3, 2040)])
+def test_routed_combine(dev, in_dtype, top, c):
+    """Eight-column vector kernel (c % 8 == 0; top 6 leaves a partial batch
+    of ranks) and the generic kernel (c = 2040), inactive rows zero."""
     import torch
     from akas_amd import ops
 
-    rng = np.random.default_rng(6)
-    rows, top, c = 33, 4, 2048
+    rng = np.random.default_rng(6 + top)
+    rows = 33
     e = rng.normal(0, 1, (rows, top, c)).astype(np.float32)
-    if in_dtype == "bfloat16":
-        e = ofp8.bf16_round(e)
+    if in_dtype != "float32":
+        e = ofp8.round_to(e, in_dtype)
     w = rng.uniform(0, 1, (rows, top)).astype(np.float32)
     active = np.ones(rows, np.int32)
     active[-1] = 0
