@@ -151,6 +151,75 @@ __global__ __launch_bounds__(1024) void routes_kernel(const int32_t* __restrict_
   if (tid == 0) counts[e] = (int32_t)used;
 }
 
+// top = 4: four consecutive rows per thread (one 16-byte load of their ids,
+// one of their activity flags), 4096 rows per pass, and the next pass's loads
+// in flight while this pass is scanned and written.  Routes come out in the
+// same (row, rank) order as the generic kernel's.
+__global__ __launch_bounds__(1024) void routes4_kernel(const int32_t* __restrict__ ids,
+                                                       const int32_t* __restrict__ active,
+                                                       int32_t* __restrict__ counts,
+                                                       int32_t* __restrict__ routes, int64_t rows) {
+  constexpr int RPT = 4, PASS = 1024 * RPT;
+  __shared__ int wave_tot[16];
+  const int e = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int32_t* out = routes + (int64_t)e * rows;
+  // rows past the end read row 0 (their flags are masked below)
+  auto load = [&](int64_t r0, int4 (&id)[RPT], int4& act) {
+    const int64_t row = r0 + (int64_t)tid * RPT;
+    const int64_t safe = row + RPT <= rows ? row : 0;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) id[i] = reinterpret_cast<const int4*>(ids)[safe + i];
+    act = *reinterpret_cast<const int4*>(active + safe);
+  };
+  int4 id[RPT], act, nid[RPT], nact;
+  load(0, id, act);
+  int64_t base = 0;
+  for (int64_t r0 = 0; r0 < rows; r0 += PASS) {
+    if (r0 + PASS < rows) load(r0 + PASS, nid, nact);
+    const int64_t row = r0 + (int64_t)tid * RPT;
+    const int a[RPT] = {act.x, act.y, act.z, act.w};
+    uint32_t mask[RPT];
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const bool live = row + i < rows && a[i] != 0;
+      const int4 v = id[i];
+      mask[i] = live ? (uint32_t)(v.x == e) | ((uint32_t)(v.y == e) << 1) |
+                           ((uint32_t)(v.z == e) << 2) | ((uint32_t)(v.w == e) << 3)
+                     : 0u;
+      cnt += __builtin_popcount(mask[i]);
+    }
+    const int incl = wave_inclusive_scan(cnt, lane);
+    if (lane == 63) wave_tot[wave] = incl;
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      const int t = wave_tot[w];
+      before += w < wave ? t : 0;
+      total += t;
+    }
+    int64_t pos = base + before + incl - cnt;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if ((mask[i] >> k) & 1u) {
+          if (pos < rows) out[pos] = (int32_t)((row + i) * 4 + k);
+          ++pos;
+        }
+    base += total;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) id[i] = nid[i];
+    act = nact;
+  }
+  const int64_t used = base < rows ? base : rows;
+  for (int64_t i = used + tid; i < rows; i += 1024) out[i] = -1;
+  if (tid == 0) counts[e] = (int32_t)used;
+}
+
 // ---------------------------------------------------------------------------
 // per-expert tile prefix (shared by the tile map and the pack kernel)
 // ---------------------------------------------------------------------------
@@ -412,8 +481,12 @@ extern "C" int akas_quantized_routes(const int32_t* ids, const int32_t* active, 
                                      void* stream) {
   if (r < 0 || experts < 1 || top < 1 || r * top > 0x7FFFFFFF) return AKAS_ERR_GEOMETRY;
   if (!counts || (r > 0 && (!ids || !active || !routes))) return AKAS_ERR_NULL;
-  routes_kernel<<<experts, 1024, 0, reinterpret_cast<hipStream_t>(stream)>>>(ids, active, counts,
-                                                                            routes, r, top);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (top == 4 && r % 4 == 0 && reinterpret_cast<uintptr_t>(active) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(ids) % 16 == 0)
+    routes4_kernel<<<experts, 1024, 0, s>>>(ids, active, counts, routes, r);
+  else
+    routes_kernel<<<experts, 1024, 0, s>>>(ids, active, counts, routes, r, top);
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }

@@ -75,7 +75,8 @@ def test_sigmoid_router(dev, normalize):
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("rows,top,experts,mult", [(1, 4, 64, 1), (33, 2, 4, 1), (1025, 4, 64, 3),
-                                                   (16384, 4, 64, 7), (257, 3, 7, 1)])
+                                                   (16384, 4, 64, 7), (257, 3, 7, 1),
+                                                   (4100, 4, 64, 5), (12, 4, 5, 1)])
 def test_quantized_routes_patterns(dev, rows, top, experts, mult):
     from akas_amd import ops
 
