@@ -103,6 +103,105 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ l
   }
 }
 
+// experts <= 64 and top <= 8: 16 rows per wave, four lanes per row, each lane
+// holding 16 expert scores in registers.  A rank's arg-max is a scan of the
+// lane's scores plus two DPP quad swaps -- no round trips through the LDS
+// crossbar.  Selection rule and weight arithmetic are router_kernel's, so
+// ids and weights are identical.
+constexpr int kQuadTop = 8;
+
+template <int CTRL>
+AKAS_DEV void quad_argmax_step(float& s, int& idx) {
+  const float os = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), CTRL, 0xF, 0xF, true));
+  const int oi = __builtin_amdgcn_update_dpp(0, idx, CTRL, 0xF, 0xF, true);
+  if (os > s || (os == s && oi < idx)) {
+    s = os;
+    idx = oi;
+  }
+}
+
+template <int SOFTMAX>
+__global__ __launch_bounds__(256) void router_quad_kernel(const float* __restrict__ logits,
+                                                          const float* __restrict__ bias,
+                                                          int32_t* __restrict__ ids,
+                                                          float* __restrict__ weights,
+                                                          int64_t rows, int experts, int top,
+                                                          float scale, int normalize) {
+  const int lane = threadIdx.x & 63, q = lane & 3;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + (lane >> 2);
+  const bool live = row < rows;
+  const float* l = logits + (live ? row : 0) * experts;  // spare lanes read row 0, never stored
+  float score[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int e = q * 16 + i;
+    float v = -__builtin_inff();
+    if (e < experts) {
+      const float b = bias ? bias[e] : 0.f;
+      if (SOFTMAX)
+        v = l[e] + b;
+      else
+        v = __fdiv_rn(1.0f, 1.0f + expf(-l[e])) + b;
+    }
+    score[i] = v;
+  }
+  float chosen[kQuadTop];
+  int chosen_id[kQuadTop];
+#pragma unroll
+  for (int rank = 0; rank < kQuadTop; ++rank) {
+    if (rank >= top) break;
+    float best = -__builtin_inff();
+    int bi = 0x7FFFFFFF;
+    // ascending expert index, so strict > keeps the lowest index on ties
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int e = q * 16 + i;
+      if (e < experts && (score[i] > best || bi == 0x7FFFFFFF)) {
+        best = score[i];
+        bi = e;
+      }
+    }
+    quad_argmax_step<0xB1>(best, bi);  // quad_perm [1,0,3,2]
+    quad_argmax_step<0x4E>(best, bi);  // quad_perm [2,3,0,1]
+    chosen_id[rank] = bi;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (q * 16 + i == bi) score[i] = -__builtin_inff();
+    const float lv = l[bi];
+    chosen[rank] = SOFTMAX ? lv : __fdiv_rn(1.0f, 1.0f + expf(-lv));
+  }
+  if (!live || q != 0) return;
+  if (SOFTMAX) {
+    float peak = chosen[0];
+#pragma unroll
+    for (int i = 1; i < kQuadTop; ++i)
+      if (i < top) peak = __builtin_fmaxf(peak, chosen[i]);
+    float total = 0.f;
+#pragma unroll
+    for (int i = 0; i < kQuadTop; ++i)
+      if (i < top) total += expf(chosen[i] - peak);
+#pragma unroll
+    for (int i = 0; i < kQuadTop; ++i)
+      if (i < top) {
+        ids[row * top + i] = chosen_id[i];
+        weights[row * top + i] = __fdiv_rn(scale * expf(chosen[i] - peak), total);
+      }
+  } else {
+    float den = normalize ? 1e-6f : 1.0f;
+    if (normalize) {
+#pragma unroll
+      for (int i = 0; i < kQuadTop; ++i)
+        if (i < top) den += chosen[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kQuadTop; ++i)
+      if (i < top) {
+        ids[row * top + i] = chosen_id[i];
+        weights[row * top + i] = __fdiv_rn(chosen[i] * scale, den);
+      }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // quantized_routes: one 1024-thread workgroup per expert, ordered block scan
 // over the rows (src/akas/ops/moe/kernel.py:121-151, cuda.py:2187-2322)
@@ -456,8 +555,13 @@ extern "C" int akas_biased_router(const float* logits, const float* bias, int32_
     return AKAS_ERR_GEOMETRY;
   if (r == 0) return AKAS_OK;
   if (!logits || !ids || !weights) return AKAS_ERR_NULL;
-  router_kernel<0><<<(int)((r + 3) / 4), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      logits, bias, ids, weights, r, experts, top, scale, normalize);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (experts <= 64 && top <= kQuadTop)
+    router_quad_kernel<0><<<(int)((r + 63) / 64), 256, 0, s>>>(logits, bias, ids, weights, r,
+                                                              experts, top, scale, normalize);
+  else
+    router_kernel<0><<<(int)((r + 3) / 4), 256, 0, s>>>(logits, bias, ids, weights, r, experts,
+                                                       top, scale, normalize);
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }
@@ -470,8 +574,13 @@ extern "C" int akas_biased_softmax_router(const float* logits, const float* bias
     return AKAS_ERR_GEOMETRY;
   if (r == 0) return AKAS_OK;
   if (!logits || !ids || !weights) return AKAS_ERR_NULL;
-  router_kernel<1><<<(int)((r + 3) / 4), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      logits, bias, ids, weights, r, experts, top, scale, 1);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (experts <= 64 && top <= kQuadTop)
+    router_quad_kernel<1><<<(int)((r + 63) / 64), 256, 0, s>>>(logits, bias, ids, weights, r,
+                                                              experts, top, scale, 1);
+  else
+    router_kernel<1><<<(int)((r + 3) / 4), 256, 0, s>>>(logits, bias, ids, weights, r, experts,
+                                                       top, scale, 1);
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }

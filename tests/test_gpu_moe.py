@@ -39,8 +39,12 @@ def pattern_routes(rows, top, experts, mult=1, inactive_last=True):
 # routers
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("rows,experts,top", [(1, 64, 4), (257, 64, 4), (64, 256, 8), (9, 7, 3)])
+@pytest.mark.parametrize("rows,experts,top", [(1, 64, 4), (257, 64, 4), (64, 256, 8), (9, 7, 3),
+                                              (1000, 64, 8), (33, 32, 6), (17, 64, 1)])
 def test_softmax_router(dev, rows, experts, top):
+    """Up to 64 experts and top 8 take the four-lanes-per-row kernel, the
+    rest the one-wave-per-row kernel; ties within a lane's experts (0, 1) and
+    across lanes (20, 40) resolve to the lower id."""
     from akas_amd import ops
 
     rng = np.random.default_rng(17)
@@ -48,6 +52,9 @@ def test_softmax_router(dev, rows, experts, top):
     bias = rng.normal(0, 0.1, experts).astype(np.float32)
     logits[0, 1] = logits[0, 0]  # forced tie resolved to the lower id
     bias[1] = bias[0]
+    if experts > 40:
+        logits[0, 20] = logits[0, 40] = 5.0
+        bias[40] = bias[20]
     ids, w = ops.biased_softmax_router(_t(logits, dev), _t(bias, dev), top=top, scale=1.5)
     eids, ew = omoe.biased_softmax_router(logits, bias, top, scale=1.5)
     np.testing.assert_array_equal(_np(ids), eids)
