@@ -167,8 +167,12 @@ AKAS_DEV void multiply(const Plan& p, Acc& acc, int a_row0, int b_row0, float ws
     if (j == 0) copy_scales<1 - S>(p, kb_next);
     const v8i bf = fragment(bt, b_row0 + 16 * j, lane);
     v4f cur[4];
+    // The wave issuing MFMAs goes first; its SIMD partner's LDS reads and
+    // folds fill the gaps (measured 5-9% faster than equal priority).
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) cur[i] = mfma_e4m3(bf, af[i]);
+    __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float c = (j & 1) ? c1[i] : c0[i];
