@@ -280,11 +280,28 @@ def cpu_baseline(budget_s=12.0):
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
     step_bytes = sum(dense_bytes(m, K_DEC, N_DEC) for m in DECODE_M)
+
+    # One thread as well (the reference's CI runs its CPU checks with
+    # OMP_NUM_THREADS=1): median of 5 sweeps.
+    def sweep1():
+        for m in DECODE_M:
+            lib.ref_fp8_linear_bf16(native.ptr(xs[m]), native.ptr(codes), native.ptr(scales),
+                                    native.ptr(outs[m]), 1, m, K_DEC, N_DEC, 1)
+
+    times1 = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        sweep1()
+        times1.append(time.perf_counter() - t0)
+    med1 = float(np.median(times1))
     return dict(value=round(step_bytes / med / 1e9, 2), unit="GB/s", cores=threads,
                 kind="port",
                 sample=f"full decode sweep (M=1,4,16,64,256; K=2048; N=6144), median of "
                        f"{len(times)} runs, {med * 1e3:.1f} ms/sweep, oracle/cpu_ref.c -O3 "
-                       f"-fopenmp f32 accumulation")
+                       f"-fopenmp f32 accumulation",
+                value_1_thread=round(step_bytes / med1 / 1e9, 3),
+                sample_1_thread=f"same sweep on 1 thread, median of 5 runs, "
+                                f"{med1 * 1e3:.1f} ms/sweep")
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_gemm_m256_counters.md")

@@ -446,3 +446,90 @@ def test_routed_moe_layer(dev, rows, packed, fused):
     exp, _, _ = omoe.moe_layer(x, logits, np.zeros(E, np.float32), *bank["w1"], *bank["w3"],
                                *bank["w2"], top)
     assert rel_fro(_np(out), exp) < 1e-2
+
+
+@pytest.mark.parametrize("rows,packed,fused,policy", [
+    (256, False, True, "bfloat16"), (256, False, False, "bfloat16"),
+    (1000, True, True, "bfloat16"), (300, False, True, "float32")])
+def test_routed_moe_layer_sigmoid_router_policies(dev, rows, packed, fused, policy):
+    """The LFM2 block's sigmoid+bias router (``src/akas/ops/moe/kernel.py:154-203``)
+    with a nonzero bias and route scale, bf16 intermediate policies
+    (``src/akas/ops/moe/definition.py:677-793``) and inactive rows, against
+    the layer equation of ``tests/support/native_fp8_reference.py:116-144``."""
+    import torch
+    from akas_amd import moe
+
+    rng = np.random.default_rng(7)
+    H, F, E, top = 512, 384, 32, 4
+    x = bf16_normal(rng, (rows, H))
+    logits = rng.normal(0, 1, (rows, E)).astype(np.float32)
+    bias = rng.normal(0, 0.5, E).astype(np.float32)
+    active = (rng.random(rows) > 0.1).astype(np.int32)
+    bank = {}
+    for name, shape in (("w1", (E, F, H)), ("w3", (E, F, H)), ("w2", (E, H, F))):
+        bank[name] = ofp8.quantize_weight_blocks(rng.normal(0, 0.05, shape).astype(np.float32))
+    wts = moe.ExpertWeights(*(_t(a, dev) for n in ("w1", "w3", "w2") for a in bank[n]))
+    dt = getattr(torch, policy)
+    out = moe.routed_moe(_t(x, dev, torch.bfloat16), _t(logits, dev), _t(bias, dev), wts,
+                         top=top, active=_t(active, dev), router="biased_router", scale=2.5,
+                         normalize=True, packed=packed, fused_swiglu=fused,
+                         product_dtype=dt, activation_dtype=dt, contribution_dtype=dt)
+    exp, ids, _ = omoe.moe_layer(x, logits, bias, *bank["w1"], *bank["w3"], *bank["w2"], top,
+                                 router="sigmoid", scale=2.5, normalize=True, active=active,
+                                 activation_dtype=policy, contribution_dtype=policy)
+    got = _np(out)
+    assert np.all(got[active == 0] == 0)
+    assert rel_fro(got, exp) < 1e-2
+
+
+# ---------------------------------------------------------------------------
+# the layer at the LFM2-MoE dimensions (H=2048, F=1536, E=64, top 4)
+# ---------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def lfm2_bank(dev):
+    """Expert banks at the benchmark's dimensions, block-quantized on the GPU
+    (N(0, 0.02) weights) with host copies of the codes and scales for the
+    oracle."""
+    import torch
+    from akas_amd import moe, ops
+
+    E, H, F = 64, 2048, 1536
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    dev_bank, host_bank = [], []
+    for n, k in ((F, H), (F, H), (H, F)):
+        codes, scales = [], []
+        for _ in range(E):
+            w = torch.randn((n, k), generator=g, device=dev, dtype=torch.float32) * 0.02
+            c, s = ops.quantize_weight_blocks(w)
+            codes.append(c)
+            scales.append(s)
+        c, s = torch.stack(codes), torch.stack(scales)
+        dev_bank += [c, s]
+        host_bank += [_np(c), _np(s)]
+    return moe.ExpertWeights(*dev_bank), host_bank
+
+
+@pytest.mark.parametrize("rows,packed,zipf", [(256, False, False), (2048, True, True)])
+def test_routed_moe_layer_lfm2_dims(dev, lfm2_bank, rows, packed, zipf):
+    """Decode (32-row expert tiles) and prefill (packed, DMA-fed 256-row
+    tiles, Zipf-skewed routing) at the real layer size with the benchmark's
+    bf16 intermediate policies, against the layer equation."""
+    import torch
+    from akas_amd import moe
+
+    wts, host = lfm2_bank
+    E, H = 64, 2048
+    rng = np.random.default_rng(3)
+    x = bf16_normal(rng, (rows, H))
+    logits = rng.normal(0, 1, (rows, E)).astype(np.float32)
+    if zipf:
+        logits += (-1.1 * np.log1p(rng.permutation(E))).astype(np.float32)[None, :]
+    bf = torch.bfloat16
+    out = moe.routed_moe(_t(x, dev, bf), _t(logits, dev), None, wts, top=4, packed=packed,
+                         max_block_m=128 if packed else 64, product_dtype=bf,
+                         activation_dtype=bf, contribution_dtype=bf)
+    exp, _, _ = omoe.moe_layer(x, logits, np.zeros(E, np.float32), *host, 4,
+                               activation_dtype="bfloat16", contribution_dtype="bfloat16")
+    assert rel_fro(_np(out), exp) < 1e-2
