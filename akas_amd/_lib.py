@@ -23,6 +23,7 @@ SIGNATURES = {
     "akas_status_string": (ctypes.c_char_p, [_i]),
     "akas_abi_count": (_i, []),
     "akas_quantize": (_i, [_p, _i, _p, _p, _i64, _i64, _p]),
+    "akas_rms_quantize": (_i, [_p, _i, _p, _i, _f, _i, _p, _i, _p, _p, _i64, _i64, _p]),
     "akas_dequantize_fp8": (_i, [_p, _p, _p, _i, _i64, _i64, _p]),
     "akas_quantize_weight_blocks": (_i, [_p, _p, _p, _i, _i64, _i64, _i64, _p]),
     "akas_fp8_linear_workspace_size": (_sz, [_i64, _i64, _i64]),

@@ -11,6 +11,8 @@
 
 namespace akas {
 
+constexpr int64_t kRmsQuantizeMaxCols = 8192;  // four waves of at most 2048 columns
+
 // One 128-group per 16 lanes; grid-stride over all groups.
 // (src/akas/quantization/activations/fp8/cuda.py:10-56, warp form :80-141)
 //
@@ -48,6 +50,104 @@ __global__ __launch_bounds__(256) void quantize_kernel(const void* __restrict__ 
     const uint2 codes = quantize8(v, s);
     *reinterpret_cast<uint2*>(out + at) = codes;
     if (lane16 == 0) scales[gi] = s;
+  }
+}
+
+// RMSNorm fused with the 1x128 quantizer (the producer step before the
+// quantizer in the LFM2 programs: kinds "rms" then "quantize").
+//   y = round_YT( (x * (1 / sqrt(sum(x^2) / cols + eps))) * w' ),
+//   w' = w, or 1 + w when zero_centered
+// (src/akas/ops/normalization/definition.py:10-31, equation of
+// normalization/validation.py:31-52), written when y != nullptr, and the
+// codes/scales of exactly those rounded values (quantize8, the quantizer's
+// own group code).
+//
+// WPR waves per row (1 up to 2048 columns, 4 beyond): wave q of a row owns
+// columns [q*span, q*span + span) with span a multiple of 128 and at most
+// 2048, and lane l holds, for chunk j, the 8 values at span offset
+// 512j + 8l .. +7, so 16 lanes own one 128-group as in the quantizer.  The
+// sum of squares is accumulated per lane in chunk order, reduced by a fixed
+// xor butterfly within the wave (every lane ends with the same total) and,
+// for WPR = 4, summed over the waves in wave order through LDS.
+template <int DT, int WT, int YT, int WPR>
+__global__ __launch_bounds__(256) void rms_quantize_kernel(const void* __restrict__ x,
+                                                           const void* __restrict__ w, float eps,
+                                                           int zero_centered, void* __restrict__ y,
+                                                           uint8_t* __restrict__ codes,
+                                                           float* __restrict__ scales,
+                                                           int64_t rows, int cols, int span) {
+  constexpr int NJ = 4;  // 4 x 512 = 2048 columns per wave at most
+  constexpr int ROWS_PER_BLOCK = 4 / WPR;
+  __shared__ float part[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = wave % WPR;
+  const int c0 = q * span, c1 = min(c0 + span, cols);
+  const int groups = cols / kBlock;
+  // every thread of a block runs the same number of iterations (WPR = 4
+  // synchronizes inside the loop)
+  for (int64_t r0 = (int64_t)blockIdx.x * ROWS_PER_BLOCK; r0 < rows; r0 += (int64_t)gridDim.x * ROWS_PER_BLOCK) {
+    const int64_t row = r0 + wave / WPR;
+    const bool live = row < rows;
+    const int64_t rbase = (live ? row : r0) * cols;
+    float v[NJ][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int col = c0 + 512 * j + 8 * lane;
+      if (live && col < c1) {
+        load8<DT>(x, rbase + col, v[j]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[j][e], v[j][e], ss);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[j][e] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if constexpr (WPR > 1) {
+      if (lane == 0) part[wave] = ss;
+      __syncthreads();
+      ss = part[0];
+#pragma unroll
+      for (int k = 1; k < WPR; ++k) ss += part[k];
+      __syncthreads();  // the next row's partials overwrite part[]
+    }
+    if (!live) continue;
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)cols) + eps));
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int col = c0 + 512 * j + 8 * lane;
+      // all 16 lanes of a group are on the same side of c1 (multiples of 128)
+      if (c0 + 512 * j + 8 * (lane & ~15) >= c1) continue;
+      float wv[8];
+      load8<WT>(w, col, wv);
+      float qv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float we = zero_centered ? 1.0f + wv[e] : wv[e];
+        qv[e] = round_t<YT>((v[j][e] * inv) * we);
+      }
+      if (y != nullptr) {
+        if constexpr (YT == AKAS_DTYPE_F32) {
+          float4* dst = reinterpret_cast<float4*>(reinterpret_cast<float*>(y) + rbase + col);
+          dst[0] = float4{qv[0], qv[1], qv[2], qv[3]};
+          dst[1] = float4{qv[4], qv[5], qv[6], qv[7]};
+        } else {
+          uint4 pk;
+          uint32_t* u = reinterpret_cast<uint32_t*>(&pk);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            u[i] = YT == AKAS_DTYPE_BF16 ? f32x2_to_bf16x2(qv[2 * i], qv[2 * i + 1])
+                                         : (f32_to_f16_bits(qv[2 * i]) | (f32_to_f16_bits(qv[2 * i + 1]) << 16));
+          *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(y) + rbase + col) = pk;
+        }
+      }
+      float sc;
+      const uint2 c8 = quantize8(qv, sc);
+      *reinterpret_cast<uint2*>(codes + rbase + col) = c8;
+      if ((lane & 15) == 0) scales[row * groups + col / kBlock] = sc;
+    }
   }
 }
 
@@ -131,6 +231,46 @@ static void launch_quantize_t(const void* x, int x_dtype, uint8_t* out, float* s
   }
 }
 
+template <int DT, int WT, int YT>
+static int launch_rms_quantize_t(const void* x, const void* w, float eps, int zero_centered, void* y,
+                                 uint8_t* codes, float* scales, int64_t rows, int cols, hipStream_t s) {
+  if (cols <= 2048) {  // one wave per row, four rows per 256-thread block
+    const int64_t want = (rows + 3) / 4;
+    const int grid = (int)(want < 16384 ? want : 16384);
+    rms_quantize_kernel<DT, WT, YT, 1><<<grid, 256, 0, s>>>(x, w, eps, zero_centered, y, codes, scales,
+                                                            rows, cols, cols);
+  } else {  // four waves per row, spans of whole 128-groups
+    const int span = (((cols + 3) / 4 + kBlock - 1) / kBlock) * kBlock;
+    const int grid = (int)(rows < 16384 ? rows : 16384);
+    rms_quantize_kernel<DT, WT, YT, 4><<<grid, 256, 0, s>>>(x, w, eps, zero_centered, y, codes, scales,
+                                                            rows, cols, span);
+  }
+  return hipGetLastError() == hipSuccess ? AKAS_OK : AKAS_ERR_LAUNCH;
+}
+
+static int launch_rms_quantize(const void* x, int x_dtype, const void* w, int w_dtype, float eps,
+                               int zero_centered, void* y, int y_dtype, uint8_t* codes, float* scales,
+                               int64_t rows, int cols, hipStream_t s) {
+  auto by_w = [&](auto XD, auto YD) {
+    constexpr int X = decltype(XD)::value, Y = decltype(YD)::value;
+    return w_dtype == AKAS_DTYPE_F32
+               ? launch_rms_quantize_t<X, AKAS_DTYPE_F32, Y>(x, w, eps, zero_centered, y, codes, scales, rows, cols, s)
+               : launch_rms_quantize_t<X, AKAS_DTYPE_BF16, Y>(x, w, eps, zero_centered, y, codes, scales, rows, cols, s);
+  };
+  auto by_y = [&](auto XD) {
+    switch (y_dtype) {
+      case AKAS_DTYPE_F32: return by_w(XD, DtypeTag<AKAS_DTYPE_F32>{});
+      case AKAS_DTYPE_F16: return by_w(XD, DtypeTag<AKAS_DTYPE_F16>{});
+      default: return by_w(XD, DtypeTag<AKAS_DTYPE_BF16>{});
+    }
+  };
+  switch (x_dtype) {
+    case AKAS_DTYPE_F32: return by_y(DtypeTag<AKAS_DTYPE_F32>{});
+    case AKAS_DTYPE_F16: return by_y(DtypeTag<AKAS_DTYPE_F16>{});
+    default: return by_y(DtypeTag<AKAS_DTYPE_BF16>{});
+  }
+}
+
 int launch_quantize(const void* x, int x_dtype, uint8_t* out, float* scales, int64_t rows,
                     int64_t k, bool fragment_major, hipStream_t s) {
   const int kb = (int)(k / kBlock);
@@ -150,6 +290,24 @@ extern "C" int akas_quantize(const void* x, int x_dtype, uint8_t* out, float* sc
   if (rows == 0) return AKAS_OK;
   if (!x || !out || !scales) return AKAS_ERR_NULL;
   return launch_quantize(x, x_dtype, out, scales, rows, k, false, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int akas_rms_quantize(const void* x, int x_dtype, const void* w, int w_dtype, float eps,
+                                 int zero_centered, void* y, int y_dtype, uint8_t* codes,
+                                 float* scales, int64_t rows, int64_t cols, void* stream) {
+  if (rows < 0 || cols <= 0 || cols % kBlock || cols > kRmsQuantizeMaxCols) return AKAS_ERR_GEOMETRY;
+  if (!float_dtype(x_dtype) || !float_dtype(y_dtype)) return AKAS_ERR_DTYPE;
+  if (w_dtype != AKAS_DTYPE_F32 && w_dtype != AKAS_DTYPE_BF16) return AKAS_ERR_DTYPE;
+  if (!(eps >= 0.f) || !(eps < __builtin_huge_valf())) return AKAS_ERR_GEOMETRY;
+  if (rows == 0) return AKAS_OK;
+  if (!x || !w || !codes || !scales) return AKAS_ERR_NULL;
+  // 16-byte loads and stores of 8-value chunks, 8-byte code stores
+  const auto misaligned = [](const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p) % a != 0; };
+  if (misaligned(x, 16) || misaligned(w, 16) || (y && misaligned(y, 16)) || misaligned(codes, 8) ||
+      misaligned(scales, 4))
+    return AKAS_ERR_GEOMETRY;
+  return launch_rms_quantize(x, x_dtype, w, w_dtype, eps, zero_centered ? 1 : 0, y, y_dtype, codes,
+                             scales, rows, (int)cols, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int akas_dequantize_fp8(const uint8_t* codes, const float* scales, void* out,

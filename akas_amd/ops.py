@@ -97,6 +97,40 @@ def quantize(x, *, top=None, out=None, scales=None):
     return out, scales
 
 
+def rms_quantize(x, weight, *, eps, zero_centered=False, normalized_dtype=torch.bfloat16,
+                 return_normalized=True, normalized=None, out=None, scales=None):
+    """RMSNorm fused with ``quantize``: ``x [r, c]`` (f32/f16/bf16), ``weight [c]``
+    (f32/bf16) -> e4m3 codes ``[r, c]``, f32 scales ``[r, c/128]`` and, with
+    ``return_normalized``, the normalized rows in ``normalized_dtype``.
+
+    ``y = x / sqrt(mean(x^2) + eps) * w`` (``1 + w`` when ``zero_centered``) is
+    rounded to ``normalized_dtype`` and the codes are ``quantize(y)`` of those
+    rounded values, bit for bit.  Fuses the kinds ``rms``
+    (src/akas/ops/normalization/definition.py:10-31) and ``quantize``
+    (src/akas/quantization/activations/fp8/cuda.py:10-56).
+    """
+    _need(x, "x", _FLOATS)
+    _need(weight, "weight", (torch.float32, torch.bfloat16))
+    if x.dim() != 2 or tuple(weight.shape) != (x.shape[1],):
+        raise ValueError("rms_quantize takes x [r, c] and weight [c]")
+    rows, cols = x.shape
+    if cols % BLOCK or cols > 8192:
+        raise ValueError("RMSNorm-quantize channels must be a multiple of 128, at most 8192")
+    if not (eps >= 0.0) or eps == float("inf"):
+        raise ValueError("eps must be finite and non-negative")
+    ydt = _torch_dtype(normalized_dtype)
+    if ydt not in _FLOATS:
+        raise ValueError("normalized_dtype must be float32, float16 or bfloat16")
+    y = _out(normalized, "normalized", (rows, cols), ydt, x) if return_normalized else None
+    out = _out(out, "out", (rows, cols), torch.uint8, x)
+    scales = _out(scales, "scales", (rows, cols // BLOCK), torch.float32, x)
+    check(_lib.load().akas_rms_quantize(_ptr(x), _dt(x.dtype), _ptr(weight), _dt(weight.dtype),
+                                        float(eps), int(bool(zero_centered)),
+                                        _ptr(y) if y is not None else None, _dt(ydt), _ptr(out),
+                                        _ptr(scales), rows, cols, _stream()), "rms_quantize")
+    return (out, scales, y) if return_normalized else (out, scales)
+
+
 def dequantize_fp8(codes, scales, *, out=None, out_dtype=None):
     """``dequantize_fp8``: ``decode(codes) * scale`` per 128-group."""
     _need(codes, "codes", torch.uint8)

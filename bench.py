@@ -11,8 +11,8 @@ step time.  Every step reads a different copy of the weights (more than
 256 MB last-level cache.
 
 Also reported (``extras``): the prefill-shape GEMMs (M=8192), the MoE decode
-layer (T=256) and the skewed MoE prefill layer (T=16384), in TFLOP/s and
-GB/s; ``roofline`` for the dominant kernel (HIP-event timing of that kernel
+layer (T=256), the skewed MoE prefill layer (T=16384) and the fused RMSNorm +
+quantizer (16384 x 2048), in TFLOP/s and GB/s; ``roofline`` for the dominant kernel (HIP-event timing of that kernel
 alone); ``cpu_baseline`` from the oracle's C restatement on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--no-extras] [--no-cpu]
@@ -251,6 +251,29 @@ def moe_layer_bench(torch, dev, tokens, zipf, steps):
                 max_expert_rows=int(counts.max()), mean_expert_rows=float(counts.mean()))
 
 
+def rms_quantize_bench(torch, dev, rows=16384, cols=2048, steps=20):
+    """RMSNorm fused with the quantizer (the producer of the MoE block's and
+    the projections' FP8 input): bf16 x in, bf16 normalized rows + codes +
+    scales out, rotating over enough row blocks to stream from HBM."""
+    from akas_amd import ops
+
+    copies = 8  # 8 x (64 + 64 + 32) MB in rotation, past the 256 MB MALL
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    xs = [torch.randn((rows, cols), generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+    w = torch.rand((cols,), generator=g, device=dev) + 0.5
+    ys = [torch.empty((rows, cols), dtype=torch.bfloat16, device=dev) for _ in range(copies)]
+    cs = [torch.empty((rows, cols), dtype=torch.uint8, device=dev) for _ in range(copies)]
+    ss = [torch.empty((rows, cols // 128), dtype=torch.float32, device=dev) for _ in range(copies)]
+    fn = lambda i: ops.rms_quantize(xs[i % copies], w, eps=1e-5, normalized=ys[i % copies],
+                                    out=cs[i % copies], scales=ss[i % copies])
+    us = time_kernel_graph(torch, fn, copies) * 1e3
+    nbytes = rows * cols * (2 + 2 + 1) + rows * (cols // 128) * 4 + cols * 4
+    del xs, ys, cs, ss
+    return dict(rows=rows, cols=cols, us=round(us, 2), gbs=round(nbytes / (us * 1e-6) / 1e9, 1),
+                frac_hbm=round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+
+
 def cpu_baseline(budget_s=12.0):
     """The oracle's C restatement of the decode sweep on the host cores."""
     import ctypes
@@ -399,7 +422,8 @@ def main():
         line["extras"] = dict(
             prefill_gemm=prefill_gemms(torch, dev, 20),
             moe_decode=moe_layer_bench(torch, dev, 256, False, 20),
-            moe_prefill_zipf=moe_layer_bench(torch, dev, 16384, True, 10))
+            moe_prefill_zipf=moe_layer_bench(torch, dev, 16384, True, 10),
+            rms_quantize=rms_quantize_bench(torch, dev))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))

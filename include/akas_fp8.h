@@ -79,6 +79,24 @@ int akas_quantize(const void* x, int x_dtype, uint8_t* out, float* scales,
                   int64_t rows, int64_t k, void* stream);
 
 /*
+ * rms_quantize: x, w -> [y,] codes, scales.  RMSNorm fused with the
+ * activation quantizer.  It has no single reference counterpart: it fuses
+ * the reference's kind "rms" (src/akas/ops/normalization/definition.py:10-31,
+ * equation normalization/validation.py:31-52) with the kind "quantize" that
+ * consumes its output (activations/fp8/cuda.py:10-56).
+ *   y = round_y(x * (1 / sqrt(sum(x^2)/cols + eps)) * w'), w' = w (or 1 + w
+ *   when zero_centered); y [rows, cols] in y_dtype is written when y != NULL;
+ *   codes [rows, cols] / scales [rows, cols/128] are quantize(y) of exactly
+ *   those rounded values, bit for bit.
+ * x f32/f16/bf16, w f32/bf16 [cols]; cols % 128 == 0 and cols <= 8192; eps
+ * finite and >= 0; x, w, y 16-byte aligned, codes 8-byte aligned (else
+ * AKAS_ERR_GEOMETRY).
+ */
+int akas_rms_quantize(const void* x, int x_dtype, const void* w, int w_dtype, float eps,
+                      int zero_centered, void* y, int y_dtype, uint8_t* codes, float* scales,
+                      int64_t rows, int64_t cols, void* stream);
+
+/*
  * dequantize_fp8: codes, scales -> out (f32/f16/bf16) = decode(code) * scale.
  * Replaces src/akas/quantization/activations/fp8/kernel.py dequantize
  * (kind "dequantize_fp8", definition.py:43-46, 61-70).

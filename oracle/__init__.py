@@ -31,6 +31,11 @@ Pinning (what each function is checked against, in ``tests/test_oracle_*.py``):
   deterministic route patterns of ``src/akas/ops/moe/validation.py:82-99`` and
   ``:606-611``, and the empty-batch invariants of ``tests/test_lfm_moe.py``.
 * ``routed_combine``: explicit per-element loop.
+* ``rms_norm`` (``norm.py``): closed forms -- a constant row maps to
+  ``sign(c) * w`` as eps -> 0 and to ``c / sqrt(c^2 + eps) * w`` exactly, the
+  mean square of the output is 1 for ``w = 1, eps = 0``, invariance under
+  scaling of a row when ``eps = 0``, ``zero_centered`` as ``w + 1``, and a
+  zero row maps to zero for ``eps > 0``.
 
 No function here is "parity unpinned".
 """

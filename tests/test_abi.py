@@ -42,6 +42,14 @@ def test_host_validation_rejects_before_launch():
     assert lib.akas_quantize(None, 2, None, None, 4, 256, None) == -2
     # zero rows is a no-op
     assert lib.akas_quantize(None, 2, None, None, 0, 256, None) == 0
+    # fused RMSNorm-quantize: channels, dtype, eps, nulls, alignment
+    assert lib.akas_rms_quantize(16, 2, 16, 0, 1e-5, 0, None, 2, 16, 16, 4, 200, None) == -1
+    assert lib.akas_rms_quantize(16, 2, 16, 0, 1e-5, 0, None, 2, 16, 16, 4, 8320, None) == -1
+    assert lib.akas_rms_quantize(16, 2, 16, 1, 1e-5, 0, None, 2, 16, 16, 4, 256, None) == -3
+    assert lib.akas_rms_quantize(16, 2, 16, 0, -1.0, 0, None, 2, 16, 16, 4, 256, None) == -1
+    assert lib.akas_rms_quantize(None, 2, 16, 0, 1e-5, 0, None, 2, 16, 16, 4, 256, None) == -2
+    assert lib.akas_rms_quantize(18, 2, 16, 0, 1e-5, 0, None, 2, 16, 16, 4, 256, None) == -1
+    assert lib.akas_rms_quantize(None, 2, None, 0, 1e-5, 0, None, 2, None, None, 0, 256, None) == 0
     # linear: o not a multiple of 16, workspace too small
     assert lib.akas_fp8_linear(1, 2, 1, 1, 0, 1, 0, 1, 1 << 30, 4, 256, 100, None) == -1
     assert lib.akas_fp8_linear(1, 2, 1, 1, 0, 1, 0, 1, 16, 4, 256, 128, None) == -5
