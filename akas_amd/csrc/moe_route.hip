@@ -475,12 +475,19 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ e
 // inputs), the loads of up to four ranks in flight before their folds; the
 // fold order (rank 0 first, one fma per rank) is the generic kernel's, so the
 // result is the same bit for bit.  c % 8 == 0 and 16-byte aligned rows.
-template <int DT>
+//
+// SHARED (moe_combine, src/akas/ops/moe/cuda.py:392-422): each rank's value
+// is rounded to bf16 before its fold, and the shared expert enters as
+// bf16(shared) / (1 + exp(-bf16(gate))) added after the ranks.
+template <int DT, bool SHARED = false>
 __global__ __launch_bounds__(256) void combine8_kernel(const void* __restrict__ experts,
                                                        const float* __restrict__ weights,
                                                        const int32_t* __restrict__ active,
                                                        float* __restrict__ out, int top,
-                                                       int64_t c) {
+                                                       int64_t c, const void* __restrict__ shared = nullptr,
+                                                       int shared_dtype = 0,
+                                                       const void* __restrict__ gate = nullptr,
+                                                       int gate_dtype = 0) {
   const int64_t row = blockIdx.y;
   const int64_t col = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
   if (col >= c) return;
@@ -515,10 +522,18 @@ __global__ __launch_bounds__(256) void combine8_kernel(const void* __restrict__ 
             v = bf16_bits_to_f32((raw[u][0][j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
           else
             v = f16_bits_to_f32((raw[u][0][j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+          if constexpr (SHARED && DT != AKAS_DTYPE_BF16) v = round_bf16(v);
           acc[j] = __builtin_fmaf(v, wv[u], acc[j]);
         }
       }
     }
+  }
+  if constexpr (SHARED) {
+    const float g = round_bf16(load_elem(gate, row, gate_dtype));
+    const float den = 1.0f + expf(-g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      acc[j] += __fdiv_rn(round_bf16(load_elem(shared, row * c + col + j, shared_dtype)), den);
   }
   float4* dst = reinterpret_cast<float4*>(out + row * c + col);
   dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
@@ -652,6 +667,41 @@ extern "C" int akas_swiglu_experts(const void* g, const void* u, int input_dtype
   const int64_t rows = r * top;
   swiglu_kernel<<<grid_for(rows * c), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
       g, u, input_dtype, out, output_dtype, rows, c, partitions, round_inputs, round_dtype);
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_moe_combine(const void* experts, int input_dtype, const float* weights,
+                                const void* shared, int shared_dtype, const void* gate,
+                                int gate_dtype, float* out, int64_t r, int top, int64_t c,
+                                void* stream) {
+  if (r < 0 || top < 1 || c <= 0 || c % 8 || r > 65535 * 64) return AKAS_ERR_GEOMETRY;
+  if (!float_dtype(input_dtype) || !float_dtype(shared_dtype) || !float_dtype(gate_dtype))
+    return AKAS_ERR_DTYPE;
+  if (r == 0) return AKAS_OK;
+  if (!experts || !weights || !shared || !gate || !out) return AKAS_ERR_NULL;
+  if (reinterpret_cast<uintptr_t>(experts) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
+    return AKAS_ERR_GEOMETRY;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const size_t esz = input_dtype == AKAS_DTYPE_F32 ? 4 : 2;
+  const size_t ssz = shared_dtype == AKAS_DTYPE_F32 ? 4 : 2;
+  const size_t gsz = gate_dtype == AKAS_DTYPE_F32 ? 4 : 2;
+  for (int64_t r0 = 0; r0 < r; r0 += 65535) {
+    const int64_t rr = r - r0 < 65535 ? r - r0 : 65535;
+    const char* ex = reinterpret_cast<const char*>(experts) + r0 * top * c * esz;
+    const char* sh = reinterpret_cast<const char*>(shared) + r0 * c * ssz;
+    const char* ga = reinterpret_cast<const char*>(gate) + r0 * gsz;
+    dim3 grid((unsigned)((c / 8 + 255) / 256), (unsigned)rr);
+    if (input_dtype == AKAS_DTYPE_F32)
+      combine8_kernel<AKAS_DTYPE_F32, true><<<grid, 256, 0, s>>>(ex, weights + r0 * top, nullptr, out + r0 * c, top, c,
+                                                                 sh, shared_dtype, ga, gate_dtype);
+    else if (input_dtype == AKAS_DTYPE_BF16)
+      combine8_kernel<AKAS_DTYPE_BF16, true><<<grid, 256, 0, s>>>(ex, weights + r0 * top, nullptr, out + r0 * c, top, c,
+                                                                  sh, shared_dtype, ga, gate_dtype);
+    else
+      combine8_kernel<AKAS_DTYPE_F16, true><<<grid, 256, 0, s>>>(ex, weights + r0 * top, nullptr, out + r0 * c, top, c,
+                                                                 sh, shared_dtype, ga, gate_dtype);
+  }
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }

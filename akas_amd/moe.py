@@ -54,25 +54,25 @@ def _all_active(rows, device):
     return _ACTIVE[key]
 
 
-def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
-               router="biased_softmax_router", scale=1.0, normalize=True, fused_swiglu=True,
-               packed=False, max_block_m=64, product_dtype=torch.float32,
-               activation_dtype=torch.float32, contribution_dtype=torch.float32,
-               return_routing=False):
-    """One routed MoE feed-forward: ``x [T, H]`` (f32/f16/bf16) -> f32 ``[T, H]``."""
-    if router not in ("biased_router", "biased_softmax_router"):
-        raise ValueError("unknown routed expert scoring")
-    if packed and not fused_swiglu:
-        raise ValueError("packing requires the fused SwiGLU pair kernel")
+@dataclass
+class SharedExpert:
+    """Dense block-FP8 shared expert: gate ``w1``/up ``w3`` ``[F, H]`` and down
+    ``w2`` ``[H, F]`` with 128x128 block scales (f32 or bf16)."""
+
+    w1: torch.Tensor
+    s1: torch.Tensor
+    w3: torch.Tensor
+    s3: torch.Tensor
+    w2: torch.Tensor
+    s2: torch.Tensor
+
+
+def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed, max_block_m,
+                          product_dtype, activation_dtype, contribution_dtype):
+    """Routes, tile map, FP8 activations and the grouped expert products:
+    ``[T, top, H]`` contributions in ``contribution_dtype``."""
     rows, hidden = x.shape
     experts = weights.experts
-    if active is None:
-        active = _all_active(rows, x.device)
-    if router == "biased_router":
-        ids, probability = ops.biased_router(logits, bias, top=top, scale=scale,
-                                             normalize=normalize)
-    else:
-        ids, probability = ops.biased_softmax_router(logits, bias, top=top, scale=scale)
     counts, routes = ops.quantized_routes(ids, active, experts=experts)
     tile_experts, tile_rows = ops.expert_tile_map(counts, r=rows, top=top,
                                                   max_block_m=max_block_m)
@@ -110,7 +110,62 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
         out=torch.empty((rows, top, hidden), dtype=ops._torch_dtype(contribution_dtype),
                         device=x.device),
         **common)
+    return contributions, counts, routes
+
+
+def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
+               router="biased_softmax_router", scale=1.0, normalize=True, fused_swiglu=True,
+               packed=False, max_block_m=64, product_dtype=torch.float32,
+               activation_dtype=torch.float32, contribution_dtype=torch.float32,
+               return_routing=False):
+    """One routed MoE feed-forward: ``x [T, H]`` (f32/f16/bf16) -> f32 ``[T, H]``."""
+    if router not in ("biased_router", "biased_softmax_router"):
+        raise ValueError("unknown routed expert scoring")
+    if packed and not fused_swiglu:
+        raise ValueError("packing requires the fused SwiGLU pair kernel")
+    rows = x.shape[0]
+    if active is None:
+        active = _all_active(rows, x.device)
+    if router == "biased_router":
+        ids, probability = ops.biased_router(logits, bias, top=top, scale=scale,
+                                             normalize=normalize)
+    else:
+        ids, probability = ops.biased_softmax_router(logits, bias, top=top, scale=scale)
+    contributions, counts, routes = _expert_contributions(
+        x, ids, active, weights, top=top, fused_swiglu=fused_swiglu, packed=packed,
+        max_block_m=max_block_m, product_dtype=product_dtype,
+        activation_dtype=activation_dtype, contribution_dtype=contribution_dtype)
     out = ops.routed_combine(contributions, probability, active)
     if return_routing:
         return out, dict(ids=ids, weights=probability, counts=counts, routes=routes)
     return out
+
+
+def shared_expert_moe(x, logits, shared_gate, weights: ExpertWeights, shared: SharedExpert, *,
+                      top, fused_swiglu=True, packed=False, max_block_m=64,
+                      contribution_dtype=torch.bfloat16):
+    """The Qwen3.5 block-fp8 MoE block: ``x [T, H]``, router ``logits [T, E]``
+    and the shared expert's gate logit ``shared_gate [T]`` (both from the
+    caller's bf16 projections) -> f32 ``[T, H]``.
+
+    Router: iterative top-k on the bf16-rounded logits, softmax over the
+    selected ones (``decode_router``, src/akas/ops/moe/cuda.py:2011-2050).
+    Routed experts as in :func:`routed_moe` (f32 products and activations);
+    the shared expert is FP8 gate/up -> SwiGLU -> FP8 down
+    (src/akas/ops/moe/definition.py:293-373 decode, :375-418 prefill); the
+    combine adds it under its sigmoid gate (``moe_combine``,
+    src/akas/ops/moe/cuda.py:392-422).  ``contribution_dtype`` bf16 loses
+    nothing: the combine rounds each contribution to bf16 first.
+    """
+    rows = x.shape[0]
+    ids, probability = ops.biased_softmax_router(logits.to(torch.bfloat16).float(), None, top=top)
+    contributions, _, _ = _expert_contributions(
+        x, ids, _all_active(rows, x.device), weights, top=top, fused_swiglu=fused_swiglu,
+        packed=packed, max_block_m=max_block_m, product_dtype=torch.float32,
+        activation_dtype=torch.float32, contribution_dtype=contribution_dtype)
+    width = shared.w1.shape[0]
+    g = ops.fp8_linear(x, shared.w1, shared.s1)
+    u = ops.fp8_linear(x, shared.w3, shared.s3)
+    activated = ops.swiglu_experts(g.view(rows, 1, width), u.view(rows, 1, width))
+    shared_out = ops.fp8_linear(activated.view(rows, width), shared.w2, shared.s2)
+    return ops.moe_combine(contributions, probability, shared_out, shared_gate)

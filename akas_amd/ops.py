@@ -469,6 +469,32 @@ def swiglu_experts(g, u, *, round_inputs=False, round_dtype=torch.float32,
     return out
 
 
+def moe_combine(experts, weights, shared, gate, *, out=None):
+    """``moe_combine(r, top, c): experts, weights, shared, gate -> out``: the
+    weighted top-k combine plus a sigmoid-gated shared expert,
+    ``sum_rank bf16(e) * w + bf16(shared) / (1 + exp(-bf16(gate)))`` in f32.
+
+    ``experts`` ``[r, top, c]``, ``shared`` ``[r, c]`` and ``gate`` ``[r]`` or
+    ``[r, 1]`` (f32/f16/bf16), ``weights`` f32 ``[r, top]``.
+    (src/akas/ops/moe/cuda.py:392-422)
+    """
+    _need(experts, "experts", _FLOATS)
+    r, top, c = experts.shape
+    if c % 8:
+        raise ValueError("moe_combine channels must be a multiple of 8")
+    _need(weights, "weights", torch.float32, (r, top))
+    _need(shared, "shared", _FLOATS, (r, c))
+    _need(gate, "gate", _FLOATS)
+    if gate.numel() != r or gate.dim() > 2:
+        raise ValueError("moe_combine gate must be [r] or [r, 1]")
+    out = _out(out, "out", (r, c), torch.float32, experts)
+    check(_lib.load().akas_moe_combine(_ptr(experts), _dt(experts.dtype), _ptr(weights),
+                                       _ptr(shared), _dt(shared.dtype), _ptr(gate),
+                                       _dt(gate.dtype), _ptr(out), r, top, c, _stream()),
+          "moe_combine")
+    return out
+
+
 def routed_combine(experts, weights, active, *, out=None):
     """``routed_combine(r, top, c[, input_dtype]): experts, weights, active -> out``.
 

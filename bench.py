@@ -11,8 +11,9 @@ step time.  Every step reads a different copy of the weights (more than
 256 MB last-level cache.
 
 Also reported (``extras``): the prefill-shape GEMMs (M=8192), the MoE decode
-layer (T=256), the skewed MoE prefill layer (T=16384) and the fused RMSNorm +
-quantizer (16384 x 2048), in TFLOP/s and GB/s; ``roofline`` for the dominant kernel (HIP-event timing of that kernel
+layer (T=256), the skewed MoE prefill layer (T=16384), the fused RMSNorm +
+quantizer (16384 x 2048) and the shared-expert (Qwen3.5 block-fp8) MoE block
+at decode (T=64, 256 experts, top 8), in TFLOP/s and GB/s; ``roofline`` for the dominant kernel (HIP-event timing of that kernel
 alone); ``cpu_baseline`` from the oracle's C restatement on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--no-extras] [--no-cpu]
@@ -251,6 +252,37 @@ def moe_layer_bench(torch, dev, tokens, zipf, steps):
                 max_expert_rows=int(counts.max()), mean_expert_rows=float(counts.mean()))
 
 
+def shared_expert_block_bench(torch, dev, tokens=64, steps=10):
+    """The Qwen3.5 block-fp8 MoE block at decode: 256 experts, top 8,
+    H=2048, F=512, plus the sigmoid-gated shared expert."""
+    from akas_amd import moe
+
+    H, F, E, top = 2048, 512, 256, 8
+    bank = {}
+    for name, (n, k), copies in (("w1", (F, H), E), ("w3", (F, H), E), ("w2", (H, F), E),
+                                 ("sw1", (F, H), 1), ("sw3", (F, H), 1), ("sw2", (H, F), 1)):
+        c, s = make_weights(torch, n, k, copies, 11, dev)
+        bank[name] = (torch.stack(c), torch.stack(s)) if copies > 1 else (c[0], s[0])
+    wts = moe.ExpertWeights(*bank["w1"], *bank["w3"], *bank["w2"])
+    shared = moe.SharedExpert(*bank["sw1"], *bank["sw3"], *bank["sw2"])
+    rng = np.random.default_rng(0)
+    x = torch.from_numpy(rng.normal(0, 1, (tokens, H)).astype(np.float32)).to(dev).to(torch.bfloat16)
+    logits = torch.from_numpy(rng.normal(0, 1, (tokens, E)).astype(np.float32)).to(dev)
+    gate = torch.from_numpy(rng.normal(0, 1, tokens).astype(np.float32)).to(dev)
+    fn = lambda i: moe.shared_expert_moe(x, logits, gate, wts, shared, top=top)
+    g = graph_of(torch, fn, 1)
+    g.replay()
+    ms = time_kernel(torch, lambda i: g.replay(), steps)
+    ids = torch.topk(logits.to(torch.bfloat16).float(), top, dim=1).indices
+    active_experts = int(torch.unique(ids).numel())
+    wbytes = (active_experts + 1) * 3 * F * H
+    del bank, wts, shared
+    return dict(T=tokens, experts=E, top=top, us=round(ms * 1e3, 2),
+                gbs=round(wbytes / (ms * 1e-3) / 1e9, 1),
+                frac_hbm=round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                active_experts=active_experts)
+
+
 def rms_quantize_bench(torch, dev, rows=16384, cols=2048, steps=20):
     """RMSNorm fused with the quantizer (the producer of the MoE block's and
     the projections' FP8 input): bf16 x in, bf16 normalized rows + codes +
@@ -423,7 +455,8 @@ def main():
             prefill_gemm=prefill_gemms(torch, dev, 20),
             moe_decode=moe_layer_bench(torch, dev, 256, False, 20),
             moe_prefill_zipf=moe_layer_bench(torch, dev, 16384, True, 10),
-            rms_quantize=rms_quantize_bench(torch, dev))
+            rms_quantize=rms_quantize_bench(torch, dev),
+            shared_expert_moe_decode=shared_expert_block_bench(torch, dev))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))

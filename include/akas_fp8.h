@@ -283,6 +283,21 @@ int akas_swiglu_experts(const void* g, const void* u, int input_dtype, void* out
                         int round_inputs, int round_dtype, void* stream);
 
 /*
+ * moe_combine(r, top, c): experts, weights, shared, gate -> out.
+ * Replaces src/akas/ops/moe/cuda.py:392-422 (decode_moe_combine, the
+ * Qwen3.5 block-fp8 MoE combine with a sigmoid-gated shared expert; test
+ * equation moe/validation.py:506-515):
+ *   out[b, col] = sum_rank bf16(experts[b, rank, col]) * weights[b, rank]
+ *                 + bf16(shared[b, col]) / (1 + exp(-bf16(gate[b])))
+ * in f32, ranks in order.  experts [r, top, c], shared [r, c], gate [r]
+ * (f32/f16/bf16 each), weights f32 [r, top], out f32 [r, c]; c % 8 == 0;
+ * experts and out 16-byte aligned.
+ */
+int akas_moe_combine(const void* experts, int input_dtype, const float* weights,
+                     const void* shared, int shared_dtype, const void* gate, int gate_dtype,
+                     float* out, int64_t r, int top, int64_t c, void* stream);
+
+/*
  * routed_combine(r, top, c[, input_dtype]): experts, weights, active -> out.
  * Replaces src/akas/ops/moe/kernel.py:206-267.  out f32 [r, c] =
  * sum over rank (serial order) of experts[r, rank, c] * weights[r, rank];

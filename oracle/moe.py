@@ -6,7 +6,7 @@ Test infrastructure only; see ``oracle/__init__.py``.
 import numpy as np
 
 from .fp8 import (
-    BLOCK, decode_e4m3, dequantize_activation, dequantize_weight, encode_e4m3,
+    BLOCK, bf16_round, decode_e4m3, dequantize_activation, dequantize_weight, encode_e4m3,
     fake_quantize, group_scales, quantize, round_to,
 )
 
@@ -326,6 +326,21 @@ def routed_combine(experts, weights, active):
     return out
 
 
+def moe_combine(experts, weights, shared, gate):
+    """Weighted top-k combine plus a sigmoid-gated shared expert:
+    ``sum_rank bf16(e) * w + bf16(shared) / (1 + exp(-bf16(gate)))``.
+    Follows ``src/akas/ops/moe/validation.py:506-515`` (kind ``moe_combine``,
+    ``cuda.py:392-422``); the rank sum is float32 in rank order."""
+    e = bf16_round(np.asarray(experts, np.float32))
+    w = np.asarray(weights, np.float32)
+    out = np.zeros((e.shape[0], e.shape[2]), np.float32)
+    for rank in range(e.shape[1]):
+        out += e[:, rank] * w[:, rank, None]
+    g = bf16_round(np.asarray(gate, np.float32).reshape(-1, 1)).astype(np.float64)
+    sh = bf16_round(np.asarray(shared, np.float32)).astype(np.float64)
+    return (out.astype(np.float64) + sh / (1.0 + np.exp(-g))).astype(np.float32)
+
+
 # --------------------------------------------------------------------------
 # the whole routed MoE layer
 # --------------------------------------------------------------------------
@@ -366,3 +381,32 @@ def moe_layer(x, logits, bias, w1, s1, w3, s3, w2, s2, top, router="softmax",
         contributions[owners, ranks] = round_to(prod, contribution_dtype)
     out = routed_combine(contributions, prob, active)
     return out, ids, prob
+
+
+def shared_expert_moe_layer(x, logits, shared_gate, w1, s1, w3, s3, w2, s2,
+                            sw1, ss1, sw3, ss3, sw2, ss2, top):
+    """The Qwen3.5 block-fp8 MoE block: routed experts selected by the
+    softmax router on bf16-rounded logits (``decode_router``,
+    ``src/akas/ops/moe/cuda.py:2011-2050``), a shared expert (FP8 gate/up,
+    SwiGLU, FP8 down; ``ops/moe/definition.py:293-373``) and ``moe_combine``
+    with the shared expert's sigmoid gate.  Returns float32 ``[T, H]``."""
+    x = np.asarray(x, np.float32)
+    T = x.shape[0]
+    logits = bf16_round(np.asarray(logits, np.float32))
+    ids, prob = biased_softmax_router(logits, np.zeros(logits.shape[1], np.float32), top)
+    source = fake_quantize(x).astype(np.float64)
+    contributions = np.zeros((T, top, w2.shape[1]), np.float32)
+    for e in range(w1.shape[0]):
+        owners, ranks = np.nonzero(ids == e)
+        if owners.size == 0:
+            continue
+        sel = source[owners]
+        g = (sel @ dequantize_weight(w1[e], s1[e]).T).astype(np.float32)
+        u = (sel @ dequantize_weight(w3[e], s3[e]).T).astype(np.float32)
+        act = fake_quantize(swiglu(g, u)).astype(np.float64)
+        contributions[owners, ranks] = (act @ dequantize_weight(w2[e], s2[e]).T).astype(np.float32)
+    g = (source @ dequantize_weight(sw1, ss1).T).astype(np.float32)
+    u = (source @ dequantize_weight(sw3, ss3).T).astype(np.float32)
+    act = fake_quantize(swiglu(g, u)).astype(np.float64)
+    shared = (act @ dequantize_weight(sw2, ss2).T).astype(np.float32)
+    return moe_combine(contributions, prob, shared, shared_gate)

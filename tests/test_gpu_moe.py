@@ -533,3 +533,71 @@ def test_routed_moe_layer_lfm2_dims(dev, lfm2_bank, rows, packed, zipf):
     exp, _, _ = omoe.moe_layer(x, logits, np.zeros(E, np.float32), *host, 4,
                                activation_dtype="bfloat16", contribution_dtype="bfloat16")
     assert rel_fro(_np(out), exp) < 1e-2
+
+
+# ---------------------------------------------------------------------------
+# the Qwen3.5 block-fp8 variant: moe_combine and the shared-expert block
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("in_dtype,shared_dtype", [("float32", "float32"), ("bfloat16", "float32"),
+                                                    ("float16", "bfloat16")])
+@pytest.mark.parametrize("rows,top,c", [(5, 8, 2048), (300, 8, 512), (1, 2, 8)])
+def test_moe_combine(dev, in_dtype, shared_dtype, rows, top, c):
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(rows + top + c)
+    e = rng.normal(0, 1, (rows, top, c)).astype(np.float32)
+    w = np.abs(rng.normal(0, 1, (rows, top))).astype(np.float32)
+    w /= w.sum(axis=1, keepdims=True)
+    sh = rng.normal(0, 1, (rows, c)).astype(np.float32)
+    g = rng.normal(0, 2, (rows, 1)).astype(np.float32)
+    et = _t(e, dev, getattr(torch, in_dtype))
+    st = _t(sh, dev, getattr(torch, shared_dtype))
+    out = ops.moe_combine(et, _t(w, dev), st, _t(g, dev))
+    exp = omoe.moe_combine(_np(et), w, _np(st), g)
+    np.testing.assert_allclose(_np(out), exp, rtol=1e-5, atol=1e-6)
+
+
+def _device_bank(dev, seed, shapes, std):
+    """Block-quantized N(0, std) weights generated on the GPU: device codes
+    and scales plus host copies for the oracle."""
+    import torch
+    from akas_amd import ops
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    dev_bank, host_bank = {}, {}
+    for name, shape in shapes.items():
+        w = torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std
+        c, s = ops.quantize_weight_blocks(w)
+        del w
+        dev_bank[name] = (c, s)
+        host_bank[name] = (_np(c), _np(s))
+    return dev_bank, host_bank
+
+
+@pytest.mark.parametrize("rows,E,H,F,packed", [(6, 32, 256, 128, False), (300, 32, 256, 128, False),
+                                              (1024, 16, 512, 256, True),
+                                              (4, 256, 2048, 512, False)])
+def test_shared_expert_moe_block(dev, rows, E, H, F, packed):
+    """The Qwen3.5 block (256 experts, top 8, o=512 at its real size for a
+    decode batch) against the block equation."""
+    import torch
+    from akas_amd import moe
+
+    rng = np.random.default_rng(rows + E)
+    top = 8
+    dbank, bank = _device_bank(dev, rows + E, {
+        "w1": (E, F, H), "w3": (E, F, H), "w2": (E, H, F),
+        "sw1": (F, H), "sw3": (F, H), "sw2": (H, F)}, 0.02 if H == 2048 else 0.05)
+    x = bf16_normal(rng, (rows, H))
+    logits = rng.normal(0, 1, (rows, E)).astype(np.float32)
+    gate = rng.normal(0, 1.5, rows).astype(np.float32)
+    wts = moe.ExpertWeights(*(a for n in ("w1", "w3", "w2") for a in dbank[n]))
+    shared = moe.SharedExpert(*(a for n in ("sw1", "sw3", "sw2") for a in dbank[n]))
+    out = moe.shared_expert_moe(_t(x, dev, torch.bfloat16), _t(logits, dev), _t(gate, dev), wts,
+                                shared, top=top, packed=packed, max_block_m=128 if packed else 64)
+    exp = omoe.shared_expert_moe_layer(x, logits, gate, *bank["w1"], *bank["w3"], *bank["w2"],
+                                       *bank["sw1"], *bank["sw3"], *bank["sw2"], top)
+    assert rel_fro(_np(out), exp) < 1e-2

@@ -315,3 +315,26 @@ def test_c_oracle_moe_layer():
     assert lib.ref_moe_layer_bf16(p(ofp8.bf16_bits(x)), p(logits), p(w1), p(s1), p(w3), p(s3), p(w2),
                                   p(s2), p(out), T, H, F, E, top, 2) == 0
     assert rel_fro(out, exp) < 1e-4
+
+
+def test_moe_combine_closed_forms():
+    """moe_combine: a saturated gate adds bf16(shared) itself, a zero gate
+    half of it, one-hot weights pick a rank, inputs are bf16-rounded first."""
+    rng = np.random.default_rng(4)
+    r, top, c = 3, 8, 16
+    experts = rng.normal(0, 1, (r, top, c)).astype(np.float32)
+    shared = rng.normal(0, 1, (r, c)).astype(np.float32)
+    onehot = np.zeros((r, top), np.float32)
+    onehot[np.arange(r), [0, 3, 7]] = 1.0
+    bf = lambda v: (np.asarray(v, np.float32).view(np.uint32) + 0x7FFF
+                    + ((np.asarray(v, np.float32).view(np.uint32) >> 16) & 1) & 0xFFFF0000).view(np.float32)
+    pick = experts[np.arange(r), [0, 3, 7]]
+    out = omoe.moe_combine(experts, onehot, shared, np.full(r, 100.0, np.float32))
+    np.testing.assert_allclose(out, bf(pick) + bf(shared), rtol=1e-6)
+    out0 = omoe.moe_combine(experts, onehot, shared, np.zeros(r, np.float32))
+    np.testing.assert_allclose(out0, bf(pick) + bf(shared) / 2, rtol=1e-6)
+    # a value between two bf16 neighbours rounds before it is weighted
+    e = np.full((1, 1, 8), 1.0 + 2.0 ** -10, np.float32)
+    got = omoe.moe_combine(e, np.ones((1, 1), np.float32), np.zeros((1, 8), np.float32),
+                           np.zeros(1, np.float32))
+    assert np.all(got == 1.0)
