@@ -89,8 +89,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
   static_assert(PAIRED || 128 % WN == 0, "a wave's columns must stay inside one scale block");
   using Plan = StagePlan<BM, BN, THREADS>;
   constexpr int STAGE = (BM + BN) * 128;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
-  __shared__ __attribute__((aligned(16))) float lds_as[2][BM];
+  // The 32-row expert partial (the decode down projection) keeps one LDS
+  // stage: 20.9 KB lets four workgroups share a CU instead of three, 38.6 ->
+  // 36.6 us at 64 experts x 1536 -> 2048.  The paired gate/up kernel was
+  // slower that way (86.8 -> 90.6 us) and keeps two.
+  constexpr int NSTAGE = (MODE == 0 && BM == 32) ? 1 : 2;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[NSTAGE * STAGE];
+  __shared__ __attribute__((aligned(16))) float lds_as[NSTAGE][BM];
   __shared__ int rows_src[BM];
   __shared__ int rows_dst[BM];
   __shared__ float row_max[PAIRED ? WAVES_N : 1][PAIRED ? BM : 1];
@@ -157,35 +162,57 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
   // prefetch would make the current multiply wait for that prefetch.
   u32x4 ra[Plan::CA], rb[Plan::CB];
   float ras, rws0, rws1 = 0.f;
-  plan.fetch(kb0, ra, rb);
-  ras = as_row[kb0];
-  float ws0 = load_scale_t<SDT>(p.ws, ws_base + kb0);
-  float ws1 = PAIRED ? load_scale_t<SDT>(p.ws2, ws_base + kb0) : 0.f;
-  plan.stash(lds, ra, rb);
-  if (tid < BM) lds_as[0][tid] = ras;
-  {
-    const int nxt = min(kb0 + 1, kb1 - 1);
-    plan.fetch(nxt, ra, rb);
-    ras = as_row[nxt];
-    rws0 = load_scale_t<SDT>(p.ws, ws_base + nxt);
-    if constexpr (PAIRED) rws1 = load_scale_t<SDT>(p.ws2, ws_base + nxt);
-  }
-  __syncthreads();
-
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const int cur = (kb - kb0) & 1;
-    mma_stage<MT, NT, PAIRED>(acc, lds + cur * STAGE, lds + cur * STAGE + BM * 128, lds_as[cur],
-                              a_row0, b_row0, ws0, lane, ws1);
-    plan.stash(lds + (cur ^ 1) * STAGE, ra, rb);
-    if (tid < BM) lds_as[cur ^ 1][tid] = ras;
-    ws0 = rws0;
-    ws1 = rws1;
-    const int nxt = min(kb + 2, kb1 - 1);
-    plan.fetch(nxt, ra, rb);
-    ras = as_row[nxt];
-    rws0 = load_scale_t<SDT>(p.ws, ws_base + nxt);
-    if constexpr (PAIRED) rws1 = load_scale_t<SDT>(p.ws2, ws_base + nxt);
+  if constexpr (NSTAGE == 1) {
+    // one stage: stash, prefetch the next k-block, barrier, multiply, barrier
+    plan.fetch(kb0, ra, rb);
+    ras = as_row[kb0];
+    rws0 = load_scale_t<SDT>(p.ws, ws_base + kb0);
+    if constexpr (PAIRED) rws1 = load_scale_t<SDT>(p.ws2, ws_base + kb0);
+    for (int kb = kb0; kb < kb1; ++kb) {
+      if (kb > kb0) __syncthreads();  // the previous multiply is done with the stage
+      plan.stash(lds, ra, rb);
+      if (tid < BM) lds_as[0][tid] = ras;
+      const float ws0 = rws0, ws1 = rws1;
+      const int nxt = min(kb + 1, kb1 - 1);
+      plan.fetch(nxt, ra, rb);
+      ras = as_row[nxt];
+      rws0 = load_scale_t<SDT>(p.ws, ws_base + nxt);
+      if constexpr (PAIRED) rws1 = load_scale_t<SDT>(p.ws2, ws_base + nxt);
+      __syncthreads();
+      mma_stage<MT, NT, PAIRED>(acc, lds, lds + BM * 128, lds_as[0], a_row0, b_row0, ws0, lane, ws1);
+    }
     __syncthreads();
+  } else {
+    plan.fetch(kb0, ra, rb);
+    ras = as_row[kb0];
+    float ws0 = load_scale_t<SDT>(p.ws, ws_base + kb0);
+    float ws1 = PAIRED ? load_scale_t<SDT>(p.ws2, ws_base + kb0) : 0.f;
+    plan.stash(lds, ra, rb);
+    if (tid < BM) lds_as[0][tid] = ras;
+    {
+      const int nxt = min(kb0 + 1, kb1 - 1);
+      plan.fetch(nxt, ra, rb);
+      ras = as_row[nxt];
+      rws0 = load_scale_t<SDT>(p.ws, ws_base + nxt);
+      if constexpr (PAIRED) rws1 = load_scale_t<SDT>(p.ws2, ws_base + nxt);
+    }
+    __syncthreads();
+
+    for (int kb = kb0; kb < kb1; ++kb) {
+      const int cur = (kb - kb0) & 1;
+      mma_stage<MT, NT, PAIRED>(acc, lds + cur * STAGE, lds + cur * STAGE + BM * 128, lds_as[cur],
+                                a_row0, b_row0, ws0, lane, ws1);
+      plan.stash(lds + (cur ^ 1) * STAGE, ra, rb);
+      if (tid < BM) lds_as[cur ^ 1][tid] = ras;
+      ws0 = rws0;
+      ws1 = rws1;
+      const int nxt = min(kb + 2, kb1 - 1);
+      plan.fetch(nxt, ra, rb);
+      ras = as_row[nxt];
+      rws0 = load_scale_t<SDT>(p.ws, ws_base + nxt);
+      if constexpr (PAIRED) rws1 = load_scale_t<SDT>(p.ws2, ws_base + nxt);
+      __syncthreads();
+    }
   }
 
   if constexpr (!PAIRED) {
