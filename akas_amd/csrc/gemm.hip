@@ -240,32 +240,38 @@ constexpr int kSplitKbw = 4;       // k-blocks per wave: 2048-deep partitions
 // multiplies).  AFIRST: activation loads ahead of the weight loads (small
 // tiles, whose activations are quick to land) or right behind them (large
 // tiles: the weights' HBM latency goes first).
-template <int MT, int NT, int PF, int AFIRST, int AF, int OUT, int SDT>
-__global__ __launch_bounds__(64 * kSplitQuarters) void dense_split_kernel(DenseArgs p) {
-  constexpr int KBW = kSplitKbw, BM = 16 * MT, BN = 16 * NT;
+//
+// MH: waves per k-quarter (1 or 2).  With MH = 2 the workgroup has eight
+// waves: wave (kq, mh) multiplies rows 16*MT*mh .. +16*MT-1 of the tile over
+// quarter kq, the two waves of a quarter each stage half of its weight
+// slice, and each SIMD holds two waves, so one wave's MFMAs overlap the
+// other's loads and folds.
+template <int MT, int NT, int PF, int AFIRST, int AF, int OUT, int SDT, int MH = 1>
+__global__ __launch_bounds__(64 * kSplitQuarters * MH) void dense_split_kernel(DenseArgs p) {
+  constexpr int KBW = kSplitKbw, BM = 16 * MT * MH, BN = 16 * NT;
   constexpr int WT = MT * NT;                        // output tiles per wave
   constexpr int WROW = KBW * kBlock;                 // bytes of a weight row per quarter
   constexpr int QUARTER = BN * WROW;                 // LDS bytes of one quarter's slice
   constexpr int RED = WT * kWave * 16;               // LDS bytes of one wave's partials
-  static_assert(BN % 2 == 0 && WROW == 512, "two 512-byte weight rows per load");
-  static_assert(RED <= QUARTER, "a wave's partials overwrite its own weight slice");
+  static_assert(BN % (2 * MH) == 0 && WROW == 512, "two 512-byte weight rows per load");
+  static_assert(MH * RED <= QUARTER, "a quarter's partials overwrite its weight slice");
   static_assert(PF >= 1 && PF <= KBW, "activation prefetch depth");
   constexpr int LDS_BYTES = kSplitQuarters * QUARTER;
   __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
 
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kq = wave;
+  const int kq = wave % kSplitQuarters, mh = wave / kSplitQuarters;
   const int tiles_m = (p.M + BM - 1) / BM, tiles_n = p.N / BN;
   // m-tiles of one column block are adjacent, so both reads of a weight
   // slice land in the same XCD's L2
   const int id = xcd_remap(blockIdx.x, tiles_m * tiles_n);
   const int tm = id % tiles_m, tn = id / tiles_m;
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * BM + mh * 16 * MT, n0 = tn * BN;  // m0: this wave's first row
   const int KB = p.K / kBlock;
   const int part = blockIdx.y;
   const int kb0 = part * p.kb_per_part + kq * KBW;
-  uint8_t* wq = lds + kq * QUARTER;  // this wave's weight slice
+  uint8_t* wq = lds + kq * QUARTER;  // this quarter's weight slice
 
   // Rows past M re-read the last row (or 16-row tile) and are never stored.
   uint32_t arow[MT];
@@ -321,10 +327,12 @@ __global__ __launch_bounds__(64 * kSplitQuarters) void dense_split_kernel(DenseA
       for (int i = 0; i < MT; ++i) araw[s][i] = load_a(i, s);
   };
 
-  // The wave's weight slice, two rows of 512 contiguous bytes per load.
-  constexpr int WLOADS = BN / 2;
+  // The wave's share of its quarter's weight slice (rows mh*BN/MH ..), two
+  // rows of 512 contiguous bytes per load.
+  constexpr int WLOADS = BN / 2 / MH;
   const int wl_row = lane >> 5, wl_chunk = lane & 31;
-  const uint8_t* wsrc = p.w + (int64_t)(n0 + wl_row) * p.K + (int64_t)kb0 * kBlock + 16 * wl_chunk;
+  const int wl_row0 = mh * (BN / MH);
+  const uint8_t* wsrc = p.w + (int64_t)(n0 + wl_row0 + wl_row) * p.K + (int64_t)kb0 * kBlock + 16 * wl_chunk;
   u32x4 wl[WLOADS];
   auto issue_w = [&]() {
 #pragma unroll
@@ -345,9 +353,10 @@ __global__ __launch_bounds__(64 * kSplitQuarters) void dense_split_kernel(DenseA
   // so the sixteen rows of a fragment read hit sixteen different banks.
 #pragma unroll
   for (int q = 0; q < WLOADS; ++q) {
-    const int rho = 2 * q + wl_row;
+    const int rho = wl_row0 + 2 * q + wl_row;
     *reinterpret_cast<u32x4*>(wq + rho * WROW + 16 * (wl_chunk ^ (rho & 15))) = wl[q];
   }
+  if constexpr (MH > 1) __syncthreads();  // the other half of the slice
 
   float sw[KBW][NT];
 #pragma unroll
@@ -393,14 +402,16 @@ __global__ __launch_bounds__(64 * kSplitQuarters) void dense_split_kernel(DenseA
 
   // Tile t = i*NT + j is summed and stored by wave t % 4, in wave order;
   // partials go through LDS over each wave's own (finished) weight slice.
-  v4f* red = reinterpret_cast<v4f*>(lds);
+  v4f* red = reinterpret_cast<v4f*>(lds) + mh * WT * kWave;
   auto slot = [&](int q, int t) { return q * (QUARTER / 16) + t * kWave + lane; };
   const int64_t obase = (int64_t)part * p.part_stride;
-  if constexpr (AF) {
-    // Fragment-major activations: the owner keeps its own partial in
-    // registers.  (With the batched form below, the compiler no longer
-    // hoists both activation refills ahead of the first multiplies in this
-    // instantiation: measured 13.2 -> 14.0 us per M=256 fp8_linear.)
+  if constexpr (MH > 1) __syncthreads();  // both waves of a quarter are done with its slice
+  if constexpr (AF && MH == 1) {
+    // Fragment-major activations, four waves: the owner keeps its own
+    // partial in registers.  (With the batched form below, the compiler no
+    // longer hoists both activation refills ahead of the first multiplies in
+    // the 128-row four-wave instantiation: measured 13.2 -> 14.0 us per M=256
+    // fp8_linear.  With eight waves the register-resident form spills.)
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -825,15 +836,18 @@ static bool split_applies(const DenseArgs& a, int parts) {
   return a.M > 16 && a.M <= 256 && split_fits(a) && parts >= 1;
 }
 
-template <int MT, int PF, int AFIRST, int AF, int OUT, int SDT>
+template <int MT, int PF, int AFIRST, int AF, int OUT, int SDT, int MH = 1>
 static void launch_split(const DenseArgs& a, int parts, hipStream_t s) {
-  const int tiles = ((a.M + 16 * MT - 1) / (16 * MT)) * (a.N / (16 * kSplitNt));
-  dense_split_kernel<MT, kSplitNt, PF, AFIRST, AF, OUT, SDT>
-      <<<dim3(tiles, parts), 64 * kSplitQuarters, 0, s>>>(a);
+  const int tiles = ((a.M + 16 * MT * MH - 1) / (16 * MT * MH)) * (a.N / (16 * kSplitNt));
+  dense_split_kernel<MT, kSplitNt, PF, AFIRST, AF, OUT, SDT, MH>
+      <<<dim3(tiles, parts), 64 * kSplitQuarters * MH, 0, s>>>(a);
 }
 
 // Row tiles of the split kernel by M (16 < M <= 256), two tiles per column
-// block so that the grid covers 256 CUs at N = 6144.
+// block so that the grid covers 256 CUs at N = 6144.  Above 128 rows the
+// 128-row tile runs on eight waves (two 64-row halves per k-quarter): M=256
+// GEMM 11.9 -> 10.8 us, fp8_linear 13.2 -> 12.7 us against four waves with
+// 128 rows each.
 template <int AF, int OUT, int SDT>
 static void launch_split_m(const DenseArgs& a, int parts, hipStream_t s) {
   if (a.M <= 32)
@@ -843,7 +857,7 @@ static void launch_split_m(const DenseArgs& a, int parts, hipStream_t s) {
   else if (a.M <= 128)
     launch_split<4, 4, 1, AF, OUT, SDT>(a, parts, s);
   else
-    launch_split<8, 2, 0, AF, OUT, SDT>(a, parts, s);
+    launch_split<4, 2, 0, AF, OUT, SDT, 2>(a, parts, s);
 }
 
 template <int OUT, int SDT>
