@@ -844,10 +844,10 @@ static void launch_split(const DenseArgs& a, int parts, hipStream_t s) {
 }
 
 // Row tiles of the split kernel by M (16 < M <= 256), two tiles per column
-// block so that the grid covers 256 CUs at N = 6144.  Above 128 rows the
-// 128-row tile runs on eight waves (two 64-row halves per k-quarter): M=256
-// GEMM 11.9 -> 10.8 us, fp8_linear 13.2 -> 12.7 us against four waves with
-// 128 rows each.
+// block so that the grid covers 256 CUs at N = 6144.  Above 64 rows the
+// tile runs on eight waves (two row halves per k-quarter): M=256 GEMM 11.9
+// -> 10.8 us and fp8_linear 13.2 -> 12.7 us, M=128 fp8_linear 10.2 -> 9.8 us
+// against four waves; at 64 rows and below eight waves were slower.
 template <int AF, int OUT, int SDT>
 static void launch_split_m(const DenseArgs& a, int parts, hipStream_t s) {
   if (a.M <= 32)
@@ -855,7 +855,7 @@ static void launch_split_m(const DenseArgs& a, int parts, hipStream_t s) {
   else if (a.M <= 64)
     launch_split<2, 4, 1, AF, OUT, SDT>(a, parts, s);
   else if (a.M <= 128)
-    launch_split<4, 4, 1, AF, OUT, SDT>(a, parts, s);
+    launch_split<2, 2, 0, AF, OUT, SDT, 2>(a, parts, s);
   else
     launch_split<4, 2, 0, AF, OUT, SDT, 2>(a, parts, s);
 }
