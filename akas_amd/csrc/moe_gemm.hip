@@ -41,6 +41,29 @@ struct ExpertArgs {
   int max_tiles, tiles_n;
 };
 
+// Row tiles over all experts (the live part of the tile list); every lane
+// returns the same total.  Same tile count per expert as locate_tile.
+AKAS_DEV int live_tiles(const int32_t* counts, int experts, int bm, int lane) {
+  int total = 0;
+  for (int e0 = 0; e0 < experts; e0 += 64) {
+    const int e = e0 + lane;
+    const int c = e < experts ? counts[e] : 0;
+    total += wave_sum_i(((c > 0 ? c : 0) + bm - 1) / bm);
+  }
+  return total;
+}
+
+// Work item of this workgroup among the live ones.  The grid is sized for the
+// most tiles the routes can produce; enumerating only the live items before
+// the XCD remap spreads them evenly over the eight XCDs (a remap over the
+// whole grid left the dead tail -- up to a quarter of the grid -- on the last
+// XCDs, idling them).  Returns -1 for a workgroup past the live items.
+AKAS_DEV int live_item(const int32_t* counts, int experts, int bm, int tiles_n, int lane) {
+  const int total = live_tiles(counts, experts, bm, lane) * tiles_n;
+  const int id = xcd_remap(blockIdx.x, total);
+  return id < total ? id : -1;
+}
+
 // (expert, tile) of logical tile t; expert = -1 when t is past the last tile.
 AKAS_DEV void locate_tile(const int32_t* counts, int experts, int bm, int t, int lane,
                           int& expert, int& tile) {
@@ -101,6 +124,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
   __shared__ float row_max[PAIRED ? WAVES_N : 1][PAIRED ? BM : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // Tiles walked fastest, so the dead tiles past each column block's live
+  // ones are spread evenly over the grid (no live-item enumeration needed).
   const int id = xcd_remap(blockIdx.x, p.max_tiles * p.tiles_n);
   const int t = id % p.max_tiles, nb = id / p.max_tiles;
   int e, tile;
@@ -309,7 +334,8 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int id = xcd_remap(blockIdx.x, p.max_tiles * p.tiles_n);
+  const int id = live_item(p.counts, p.E, BM, p.tiles_n, lane);
+  if (id < 0) return;  // past the live items (uniform)
   const int nb = id % p.tiles_n, t = id / p.tiles_n;
   int e, tile;
   locate_tile(p.counts, p.E, BM, t, lane, e, tile);
