@@ -13,24 +13,60 @@ namespace akas {
 // routers: one wave per token row
 // ---------------------------------------------------------------------------
 
-// (score, index) arg-max across the wave: larger score wins, ties -> lower index.
+// (score, index) pairs: the larger score wins, ties -> the lower index.  One
+// DPP step combines each lane with the lane CTRL selects.
+template <int CTRL>
+AKAS_DEV void argmax_step(float& s, int& idx) {
+  const float os = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), CTRL, 0xF, 0xF, true));
+  const int oi = __builtin_amdgcn_update_dpp(0, idx, CTRL, 0xF, 0xF, true);
+  if (os > s || (os == s && oi < idx)) {
+    s = os;
+    idx = oi;
+  }
+}
+
+// Arg-max over a 16-lane DPP row: quad swaps, then half-row and row mirrors.
+AKAS_DEV void row_argmax(float& s, int& idx) {
+  argmax_step<0xB1>(s, idx);   // quad_perm [1,0,3,2]
+  argmax_step<0x4E>(s, idx);   // quad_perm [2,3,0,1]
+  argmax_step<0x141>(s, idx);  // row_half_mirror: lane i <- 7 - i within 8 lanes
+  argmax_step<0x140>(s, idx);  // row_mirror: lane i <- 15 - i within 16 lanes
+}
+
+// Arg-max across the wave: the four row results are read out as uniform values
+// and combined in order; every lane returns the same pair.
 AKAS_DEV void wave_argmax(float& s, int& idx) {
+  row_argmax(s, idx);
+  float bs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+  int bi = __builtin_amdgcn_readlane(idx, 0);
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float os = __shfl_xor(s, o, 64);
-    const int oi = __shfl_xor(idx, o, 64);
-    if (os > s || (os == s && oi < idx)) {
-      s = os;
-      idx = oi;
+  for (int r = 1; r < 4; ++r) {
+    const float os = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 16 * r));
+    const int oi = __builtin_amdgcn_readlane(idx, 16 * r);
+    if (os > bs || (os == bs && oi < bi)) {
+      bs = os;
+      bi = oi;
     }
   }
+  s = bs;
+  idx = bi;
+}
+
+// Bitwise OR over a 16-lane DPP row (same steps as row_argmax).
+template <int CTRL>
+AKAS_DEV uint32_t or_step(uint32_t v) {
+  return v | (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
 }
 
 constexpr int kMaxExpertSlots = 16;  // experts <= 64 * 16 = 1024
 constexpr int kMaxTop = 32;
 
 // Iterative top-k by maximum with lowest-index ties
-// (src/akas/ops/moe/kernel.py:176-193, :467-483).
+// (src/akas/ops/moe/kernel.py:176-193, :467-483), one wave per row, lane l
+// holding experts l, l + 64, ...  The chosen expert's value is read out of
+// its owner lane's registers (no load after the arg-max), and lane `rank`
+// keeps rank's value and id, so the top-k lives in registers without a
+// per-rank array.  Weights: the rank-ordered sums of the reference.
 template <int SOFTMAX>
 __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ logits,
                                                      const float* __restrict__ bias,
@@ -40,25 +76,25 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ l
                                                      int normalize) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  if (row >= rows) return;  // uniform per wave
   const float* l = logits + row * experts;
-  float score[kMaxExpertSlots];
+  // base: the value a chosen expert contributes (the logit, or its sigmoid);
+  // score: base + bias, the selection key.
+  float base[kMaxExpertSlots], score[kMaxExpertSlots];
   const int slots = (experts + 63) / 64;
 #pragma unroll
   for (int s = 0; s < kMaxExpertSlots; ++s) {
     const int e = s * 64 + lane;
-    float v = -__builtin_inff();
+    float v = 0.f, sc = -__builtin_inff();
     if (s < slots && e < experts) {
-      const float b = bias ? bias[e] : 0.f;
-      if (SOFTMAX)
-        v = l[e] + b;
-      else
-        v = __fdiv_rn(1.0f, 1.0f + expf(-l[e])) + b;
+      v = SOFTMAX ? l[e] : __fdiv_rn(1.0f, 1.0f + expf(-l[e]));
+      sc = v + (bias ? bias[e] : 0.f);
     }
-    score[s] = v;
+    base[s] = v;
+    score[s] = sc;
   }
-  float chosen[kMaxTop];
-  int chosen_id[kMaxTop];
+  float mine = 0.f;
+  int mine_id = 0;
   for (int rank = 0; rank < top; ++rank) {
     float best = -__builtin_inff();
     int bi = 0x7FFFFFFF;
@@ -72,133 +108,142 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ l
       }
     }
     wave_argmax(best, bi);
-    chosen_id[rank] = bi;
-    if ((bi & 63) == lane) {
+    const int owner = bi & 63, slot = bi >> 6;  // uniform
+    float v = 0.f;
 #pragma unroll
-      for (int s = 0; s < kMaxExpertSlots; ++s)
-        if (s == (bi >> 6)) score[s] = -__builtin_inff();
+    for (int s = 0; s < kMaxExpertSlots; ++s)
+      if (s == slot) {
+        v = base[s];
+        if (lane == owner) score[s] = -__builtin_inff();
+      }
+    v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), owner));
+    if (lane == rank) {
+      mine = v;
+      mine_id = bi;
     }
-    const float lv = l[bi];
-    chosen[rank] = SOFTMAX ? lv : __fdiv_rn(1.0f, 1.0f + expf(-lv));
   }
-  if (lane == 0) {
-    if (SOFTMAX) {
-      float peak = chosen[0];
-      for (int i = 1; i < top; ++i) peak = __builtin_fmaxf(peak, chosen[i]);
-      float total = 0.f;
-      for (int i = 0; i < top; ++i) total += expf(chosen[i] - peak);
-      for (int i = 0; i < top; ++i) {
-        ids[row * top + i] = chosen_id[i];
-        weights[row * top + i] = __fdiv_rn(scale * expf(chosen[i] - peak), total);
-      }
-    } else {
-      float den = normalize ? 1e-6f : 1.0f;
-      if (normalize)
-        for (int i = 0; i < top; ++i) den += chosen[i];
-      for (int i = 0; i < top; ++i) {
-        ids[row * top + i] = chosen_id[i];
-        weights[row * top + i] = __fdiv_rn(chosen[i] * scale, den);
-      }
-    }
+  float w;
+  if (SOFTMAX) {
+    float peak = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), 0));
+    for (int i = 1; i < top; ++i)
+      peak = __builtin_fmaxf(peak, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), i)));
+    const float ex = expf(mine - peak);
+    float total = 0.f;
+    for (int i = 0; i < top; ++i) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), i));
+    w = __fdiv_rn(scale * ex, total);
+  } else {
+    float den = normalize ? 1e-6f : 1.0f;
+    if (normalize)
+      for (int i = 0; i < top; ++i) den += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), i));
+    w = __fdiv_rn(mine * scale, den);
+  }
+  if (lane < top) {
+    ids[row * top + lane] = mine_id;
+    weights[row * top + lane] = w;
   }
 }
 
-// experts <= 64 and top <= 8: 16 rows per wave, four lanes per row, each lane
-// holding 16 expert scores in registers.  A rank's arg-max is a scan of the
-// lane's scores plus two DPP quad swaps -- no round trips through the LDS
-// crossbar.  Selection rule and weight arithmetic are router_kernel's, so
-// ids and weights are identical.
-constexpr int kQuadTop = 8;
-
-template <int CTRL>
-AKAS_DEV void quad_argmax_step(float& s, int& idx) {
-  const float os = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), CTRL, 0xF, 0xF, true));
-  const int oi = __builtin_amdgcn_update_dpp(0, idx, CTRL, 0xF, 0xF, true);
-  if (os > s || (os == s && oi < idx)) {
-    s = os;
-    idx = oi;
-  }
-}
+// experts <= 64 and top <= 8: four rows per wave, sixteen lanes per row (one
+// DPP row), each lane holding four consecutive experts.  A rank's arg-max is
+// a four-way scan of the lane's scores plus four DPP steps over the row (quad
+// swaps, then half-row and row mirrors); the chosen expert's value reaches
+// every lane of the row by OR-ing bit patterns over the same steps (the other
+// lanes contribute zero bits), so nothing waits on a load after the
+// arg-max.  Per wave that is a short instruction stream, which is what the
+// decode-sized router's latency is made of.  Selection rule and weight
+// arithmetic are router_kernel's, so ids and weights are identical.
+constexpr int kRowTop = 8;
 
 template <int SOFTMAX>
-__global__ __launch_bounds__(256) void router_quad_kernel(const float* __restrict__ logits,
-                                                          const float* __restrict__ bias,
-                                                          int32_t* __restrict__ ids,
-                                                          float* __restrict__ weights,
-                                                          int64_t rows, int experts, int top,
-                                                          float scale, int normalize) {
-  const int lane = threadIdx.x & 63, q = lane & 3;
-  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 16 + (lane >> 2);
+__global__ __launch_bounds__(256) void router_row16_kernel(const float* __restrict__ logits,
+                                                           const float* __restrict__ bias,
+                                                           int32_t* __restrict__ ids,
+                                                           float* __restrict__ weights,
+                                                           int64_t rows, int experts, int top,
+                                                           float scale, int normalize) {
+  const int lane = threadIdx.x & 63, l = lane & 15;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
   const bool live = row < rows;
-  const float* l = logits + (live ? row : 0) * experts;  // spare lanes read row 0, never stored
-  float score[16];
+  const float* lg = logits + (live ? row : 0) * experts;  // spare rows read row 0, never stored
+  // base: the value a chosen expert contributes (the logit, or its sigmoid);
+  // score: base + bias, the selection key.
+  float base[4], score[4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int e = q * 16 + i;
-    float v = -__builtin_inff();
+  for (int i = 0; i < 4; ++i) {
+    const int e = l * 4 + i;
+    float v = 0.f, sc = -__builtin_inff();
     if (e < experts) {
-      const float b = bias ? bias[e] : 0.f;
-      if (SOFTMAX)
-        v = l[e] + b;
-      else
-        v = __fdiv_rn(1.0f, 1.0f + expf(-l[e])) + b;
+      v = SOFTMAX ? lg[e] : __fdiv_rn(1.0f, 1.0f + expf(-lg[e]));
+      sc = v + (bias ? bias[e] : 0.f);
     }
-    score[i] = v;
+    base[i] = v;
+    score[i] = sc;
   }
-  float chosen[kQuadTop];
-  int chosen_id[kQuadTop];
+  float chosen[kRowTop];
+  int chosen_id[kRowTop];
 #pragma unroll
-  for (int rank = 0; rank < kQuadTop; ++rank) {
-    if (rank >= top) break;
+  for (int rank = 0; rank < kRowTop; ++rank) {
+    chosen[rank] = 0.f;
+    chosen_id[rank] = 0;
+    if (rank >= top) continue;
     float best = -__builtin_inff();
     int bi = 0x7FFFFFFF;
     // ascending expert index, so strict > keeps the lowest index on ties
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int e = q * 16 + i;
+    for (int i = 0; i < 4; ++i) {
+      const int e = l * 4 + i;
       if (e < experts && (score[i] > best || bi == 0x7FFFFFFF)) {
         best = score[i];
         bi = e;
       }
     }
-    quad_argmax_step<0xB1>(best, bi);  // quad_perm [1,0,3,2]
-    quad_argmax_step<0x4E>(best, bi);  // quad_perm [2,3,0,1]
+    row_argmax(best, bi);
     chosen_id[rank] = bi;
+    uint32_t bits = 0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-      if (q * 16 + i == bi) score[i] = -__builtin_inff();
-    const float lv = l[bi];
-    chosen[rank] = SOFTMAX ? lv : __fdiv_rn(1.0f, 1.0f + expf(-lv));
+    for (int i = 0; i < 4; ++i)
+      if (l * 4 + i == bi) {
+        bits = __float_as_uint(base[i]);
+        score[i] = -__builtin_inff();
+      }
+    bits = or_step<0xB1>(bits);
+    bits = or_step<0x4E>(bits);
+    bits = or_step<0x141>(bits);
+    bits = or_step<0x140>(bits);
+    chosen[rank] = __uint_as_float(bits);
   }
-  if (!live || q != 0) return;
+  // Lane l of the row stores rank l.
+  float mine = 0.f;
+  int mine_id = 0;
+#pragma unroll
+  for (int i = 0; i < kRowTop; ++i)
+    if (i == l) {
+      mine = chosen[i];
+      mine_id = chosen_id[i];
+    }
+  float w;
   if (SOFTMAX) {
     float peak = chosen[0];
 #pragma unroll
-    for (int i = 1; i < kQuadTop; ++i)
+    for (int i = 1; i < kRowTop; ++i)
       if (i < top) peak = __builtin_fmaxf(peak, chosen[i]);
     float total = 0.f;
 #pragma unroll
-    for (int i = 0; i < kQuadTop; ++i)
+    for (int i = 0; i < kRowTop; ++i)
       if (i < top) total += expf(chosen[i] - peak);
-#pragma unroll
-    for (int i = 0; i < kQuadTop; ++i)
-      if (i < top) {
-        ids[row * top + i] = chosen_id[i];
-        weights[row * top + i] = __fdiv_rn(scale * expf(chosen[i] - peak), total);
-      }
+    w = __fdiv_rn(scale * expf(mine - peak), total);
   } else {
     float den = normalize ? 1e-6f : 1.0f;
     if (normalize) {
 #pragma unroll
-      for (int i = 0; i < kQuadTop; ++i)
+      for (int i = 0; i < kRowTop; ++i)
         if (i < top) den += chosen[i];
     }
-#pragma unroll
-    for (int i = 0; i < kQuadTop; ++i)
-      if (i < top) {
-        ids[row * top + i] = chosen_id[i];
-        weights[row * top + i] = __fdiv_rn(chosen[i] * scale, den);
-      }
+    w = __fdiv_rn(mine * scale, den);
+  }
+  if (live && l < top) {
+    ids[row * top + l] = mine_id;
+    weights[row * top + l] = w;
   }
 }
 
@@ -571,9 +616,9 @@ extern "C" int akas_biased_router(const float* logits, const float* bias, int32_
   if (r == 0) return AKAS_OK;
   if (!logits || !ids || !weights) return AKAS_ERR_NULL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (experts <= 64 && top <= kQuadTop)
-    router_quad_kernel<0><<<(int)((r + 63) / 64), 256, 0, s>>>(logits, bias, ids, weights, r,
-                                                              experts, top, scale, normalize);
+  if (experts <= 64 && top <= kRowTop)
+    router_row16_kernel<0><<<(int)((r + 15) / 16), 256, 0, s>>>(logits, bias, ids, weights, r,
+                                                               experts, top, scale, normalize);
   else
     router_kernel<0><<<(int)((r + 3) / 4), 256, 0, s>>>(logits, bias, ids, weights, r, experts,
                                                        top, scale, normalize);
@@ -590,9 +635,9 @@ extern "C" int akas_biased_softmax_router(const float* logits, const float* bias
   if (r == 0) return AKAS_OK;
   if (!logits || !ids || !weights) return AKAS_ERR_NULL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (experts <= 64 && top <= kQuadTop)
-    router_quad_kernel<1><<<(int)((r + 63) / 64), 256, 0, s>>>(logits, bias, ids, weights, r,
-                                                              experts, top, scale, 1);
+  if (experts <= 64 && top <= kRowTop)
+    router_row16_kernel<1><<<(int)((r + 15) / 16), 256, 0, s>>>(logits, bias, ids, weights, r,
+                                                               experts, top, scale, 1);
   else
     router_kernel<1><<<(int)((r + 3) / 4), 256, 0, s>>>(logits, bias, ids, weights, r, experts,
                                                        top, scale, 1);

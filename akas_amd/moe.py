@@ -5,10 +5,17 @@ policy rewrites that the LFM2-MoE decode/prefill programs use
 (``fused_swiglu``, ``packed``, bf16 intermediate dtypes;
 src/akas/ops/moe/definition.py:442-540, 677-793, 951-1053):
 
-    router -> quantized_routes -> expert_tile_map -> quantize(x)
+    router -> quantized_routes -> quantize(x)
       [-> expert_pack] -> fp8_expert_swiglu (or expert_partial x2 ->
       swiglu_experts -> quantize) -> expert_partial(down, routed_input)
       -> routed_combine
+
+The reference program also builds ``expert_tile_map`` between the routes and
+the products, because its grouped kernels read their (expert, row tile) from
+it.  Here every grouped kernel locates its tile from ``counts`` on the
+device, so the block passes no tile map and skips that launch;
+``ops.expert_tile_map`` stays available, bit-exact, for callers that want the
+table itself.
 """
 
 from dataclasses import dataclass
@@ -69,13 +76,12 @@ class SharedExpert:
 
 def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed, max_block_m,
                           product_dtype, activation_dtype, contribution_dtype):
-    """Routes, tile map, FP8 activations and the grouped expert products:
+    """Routes, FP8 activations and the grouped expert products:
     ``[T, top, H]`` contributions in ``contribution_dtype``."""
     rows, hidden = x.shape
     experts = weights.experts
     counts, routes = ops.quantized_routes(ids, active, experts=experts)
-    tile_experts, tile_rows = ops.expert_tile_map(counts, r=rows, top=top,
-                                                  max_block_m=max_block_m)
+    tile_experts = tile_rows = None  # the kernels locate tiles from counts
     codes, scales = ops.quantize(x)
     common = dict(r=rows, top=top, max_block_m=max_block_m)
     offsets = None

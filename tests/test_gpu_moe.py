@@ -42,7 +42,7 @@ def pattern_routes(rows, top, experts, mult=1, inactive_last=True):
 @pytest.mark.parametrize("rows,experts,top", [(1, 64, 4), (257, 64, 4), (64, 256, 8), (9, 7, 3),
                                               (1000, 64, 8), (33, 32, 6), (17, 64, 1)])
 def test_softmax_router(dev, rows, experts, top):
-    """Up to 64 experts and top 8 take the four-lanes-per-row kernel, the
+    """Up to 64 experts and top 8 take the sixteen-lanes-per-row kernel, the
     rest the one-wave-per-row kernel; ties within a lane's experts (0, 1) and
     across lanes (20, 40) resolve to the lower id."""
     from akas_amd import ops
