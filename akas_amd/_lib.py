@@ -32,6 +32,7 @@ SIGNATURES = {
     "akas_projection_merge": (_i, [_p, _p, _i, _i64, _i64, _i, _p]),
     "akas_biased_router": (_i, [_p, _p, _p, _p, _i64, _i, _i, _f, _i, _p]),
     "akas_biased_softmax_router": (_i, [_p, _p, _p, _p, _i64, _i, _i, _f, _p]),
+    "akas_router": (_i, [_p, _p, _p, _i64, _i, _i, _p]),
     "akas_quantized_routes": (_i, [_p, _p, _p, _p, _i64, _i, _i, _p]),
     "akas_expert_tile_map": (_i, [_p, _p, _p, _i64, _i, _i, _i, _p]),
     "akas_expert_pack": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i, _i, _i64, _i, _i,

@@ -63,11 +63,13 @@ constexpr int kMaxTop = 32;
 
 // Iterative top-k by maximum with lowest-index ties
 // (src/akas/ops/moe/kernel.py:176-193, :467-483), one wave per row, lane l
-// holding experts l, l + 64, ...  The chosen expert's value is read out of
+// holding experts l, l + 64, ... (SLOTS per lane: experts <= 64 * SLOTS).
+// BF16: the logits are rounded to bf16 on load (the block-fp8 "router" kind,
+// src/akas/ops/moe/cuda.py:2011-2050).  The chosen expert's value is read out of
 // its owner lane's registers (no load after the arg-max), and lane `rank`
 // keeps rank's value and id, so the top-k lives in registers without a
 // per-rank array.  Weights: the rank-ordered sums of the reference.
-template <int SOFTMAX>
+template <int SOFTMAX, int SLOTS, int BF16>
 __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ logits,
                                                      const float* __restrict__ bias,
                                                      int32_t* __restrict__ ids,
@@ -80,14 +82,14 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ l
   const float* l = logits + row * experts;
   // base: the value a chosen expert contributes (the logit, or its sigmoid);
   // score: base + bias, the selection key.
-  float base[kMaxExpertSlots], score[kMaxExpertSlots];
+  float base[SLOTS], score[SLOTS];
   const int slots = (experts + 63) / 64;
 #pragma unroll
-  for (int s = 0; s < kMaxExpertSlots; ++s) {
+  for (int s = 0; s < SLOTS; ++s) {
     const int e = s * 64 + lane;
     float v = 0.f, sc = -__builtin_inff();
     if (s < slots && e < experts) {
-      v = SOFTMAX ? l[e] : __fdiv_rn(1.0f, 1.0f + expf(-l[e]));
+      v = SOFTMAX ? (BF16 ? round_bf16(l[e]) : l[e]) : __fdiv_rn(1.0f, 1.0f + expf(-l[e]));
       sc = v + (bias ? bias[e] : 0.f);
     }
     base[s] = v;
@@ -100,7 +102,7 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ l
     int bi = 0x7FFFFFFF;
     // slots ascend in expert index, so strict > keeps the lowest index on ties
 #pragma unroll
-    for (int s = 0; s < kMaxExpertSlots; ++s) {
+    for (int s = 0; s < SLOTS; ++s) {
       const int e = s * 64 + lane;
       if (s < slots && e < experts && (score[s] > best || bi == 0x7FFFFFFF)) {
         best = score[s];
@@ -111,7 +113,7 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ l
     const int owner = bi & 63, slot = bi >> 6;  // uniform
     float v = 0.f;
 #pragma unroll
-    for (int s = 0; s < kMaxExpertSlots; ++s)
+    for (int s = 0; s < SLOTS; ++s)
       if (s == slot) {
         v = base[s];
         if (lane == owner) score[s] = -__builtin_inff();
@@ -154,7 +156,7 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ l
 // arithmetic are router_kernel's, so ids and weights are identical.
 constexpr int kRowTop = 8;
 
-template <int SOFTMAX>
+template <int SOFTMAX, int BF16>
 __global__ __launch_bounds__(256) void router_row16_kernel(const float* __restrict__ logits,
                                                            const float* __restrict__ bias,
                                                            int32_t* __restrict__ ids,
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(256) void router_row16_kernel(const float* __restri
     const int e = l * 4 + i;
     float v = 0.f, sc = -__builtin_inff();
     if (e < experts) {
-      v = SOFTMAX ? lg[e] : __fdiv_rn(1.0f, 1.0f + expf(-lg[e]));
+      v = SOFTMAX ? (BF16 ? round_bf16(lg[e]) : lg[e]) : __fdiv_rn(1.0f, 1.0f + expf(-lg[e]));
       sc = v + (bias ? bias[e] : 0.f);
     }
     base[i] = v;
@@ -607,21 +609,39 @@ bool valid_block(int m) { return m == 4 || m == 8 || m == 16 || m == 32 || m == 
 
 using namespace akas;
 
+// One row-per-16-lanes launch for <= 64 experts and top <= 8, else one wave
+// per row with 4 or 16 expert slots per lane.
+template <int SOFTMAX, int BF16>
+static void launch_router(const float* logits, const float* bias, int32_t* ids, float* weights,
+                          int64_t r, int experts, int top, float scale, int normalize,
+                          hipStream_t s) {
+  if (experts <= 64 && top <= kRowTop)
+    router_row16_kernel<SOFTMAX, BF16><<<(int)((r + 15) / 16), 256, 0, s>>>(
+        logits, bias, ids, weights, r, experts, top, scale, normalize);
+  else if (experts <= 256)
+    router_kernel<SOFTMAX, 4, BF16><<<(int)((r + 3) / 4), 256, 0, s>>>(
+        logits, bias, ids, weights, r, experts, top, scale, normalize);
+  else
+    router_kernel<SOFTMAX, kMaxExpertSlots, BF16><<<(int)((r + 3) / 4), 256, 0, s>>>(
+        logits, bias, ids, weights, r, experts, top, scale, normalize);
+}
+
+static int check_router(const float* logits, int32_t* ids, float* weights, int64_t r,
+                        int experts, int top) {
+  if (r < 0 || experts < 1 || experts > 64 * kMaxExpertSlots || top < 1 || top > experts ||
+      top > kMaxTop || (r + 3) / 4 > 0x7FFFFFFF)
+    return AKAS_ERR_GEOMETRY;
+  if (r > 0 && (!logits || !ids || !weights)) return AKAS_ERR_NULL;
+  return AKAS_OK;
+}
+
 extern "C" int akas_biased_router(const float* logits, const float* bias, int32_t* ids,
                                   float* weights, int64_t r, int experts, int top, float scale,
                                   int normalize, void* stream) {
-  if (r < 0 || experts < 1 || experts > 64 * kMaxExpertSlots || top < 1 || top > experts ||
-      top > kMaxTop)
-    return AKAS_ERR_GEOMETRY;
-  if (r == 0) return AKAS_OK;
-  if (!logits || !ids || !weights) return AKAS_ERR_NULL;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (experts <= 64 && top <= kRowTop)
-    router_row16_kernel<0><<<(int)((r + 15) / 16), 256, 0, s>>>(logits, bias, ids, weights, r,
-                                                               experts, top, scale, normalize);
-  else
-    router_kernel<0><<<(int)((r + 3) / 4), 256, 0, s>>>(logits, bias, ids, weights, r, experts,
-                                                       top, scale, normalize);
+  const int st = check_router(logits, ids, weights, r, experts, top);
+  if (st != AKAS_OK || r == 0) return st;
+  launch_router<0, 0>(logits, bias, ids, weights, r, experts, top, scale, normalize,
+                      reinterpret_cast<hipStream_t>(stream));
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }
@@ -629,18 +649,20 @@ extern "C" int akas_biased_router(const float* logits, const float* bias, int32_
 extern "C" int akas_biased_softmax_router(const float* logits, const float* bias, int32_t* ids,
                                           float* weights, int64_t r, int experts, int top,
                                           float scale, void* stream) {
-  if (r < 0 || experts < 1 || experts > 64 * kMaxExpertSlots || top < 1 || top > experts ||
-      top > kMaxTop)
-    return AKAS_ERR_GEOMETRY;
-  if (r == 0) return AKAS_OK;
-  if (!logits || !ids || !weights) return AKAS_ERR_NULL;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (experts <= 64 && top <= kRowTop)
-    router_row16_kernel<1><<<(int)((r + 15) / 16), 256, 0, s>>>(logits, bias, ids, weights, r,
-                                                               experts, top, scale, 1);
-  else
-    router_kernel<1><<<(int)((r + 3) / 4), 256, 0, s>>>(logits, bias, ids, weights, r, experts,
-                                                       top, scale, 1);
+  const int st = check_router(logits, ids, weights, r, experts, top);
+  if (st != AKAS_OK || r == 0) return st;
+  launch_router<1, 0>(logits, bias, ids, weights, r, experts, top, scale, 1,
+                      reinterpret_cast<hipStream_t>(stream));
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_router(const float* logits, int32_t* ids, float* weights, int64_t r,
+                           int experts, int top, void* stream) {
+  const int st = check_router(logits, ids, weights, r, experts, top);
+  if (st != AKAS_OK || r == 0) return st;
+  launch_router<1, 1>(logits, nullptr, ids, weights, r, experts, top, 1.0f, 1,
+                      reinterpret_cast<hipStream_t>(stream));
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }

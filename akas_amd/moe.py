@@ -164,7 +164,7 @@ def shared_expert_moe(x, logits, shared_gate, weights: ExpertWeights, shared: Sh
     nothing: the combine rounds each contribution to bf16 first.
     """
     rows = x.shape[0]
-    ids, probability = ops.biased_softmax_router(logits.to(torch.bfloat16).float(), None, top=top)
+    ids, probability = ops.router(logits, top=top)
     contributions, _, _ = _expert_contributions(
         x, ids, _all_active(rows, x.device), weights, top=top, fused_swiglu=fused_swiglu,
         packed=packed, max_block_m=max_block_m, product_dtype=torch.float32,

@@ -284,6 +284,19 @@ def biased_softmax_router(logits, bias, *, top, scale=1.0, ids=None, weights=Non
     return ids, weights
 
 
+def router(logits, *, top, ids=None, weights=None):
+    """``router(r, experts, top): logits -> ids, weights``, the block-fp8
+    decode variant's router: selection on the bf16-rounded f32 logits, softmax
+    over the selected ones (src/akas/ops/moe/cuda.py:2011-2050)."""
+    _need(logits, "logits", torch.float32)
+    r, experts = logits.shape
+    ids = _out(ids, "ids", (r, top), torch.int32, logits)
+    weights = _out(weights, "weights", (r, top), torch.float32, logits)
+    check(_lib.load().akas_router(_ptr(logits), _ptr(ids), _ptr(weights), r, experts, top,
+                                  _stream()), "router")
+    return ids, weights
+
+
 def quantized_routes(ids, active, *, experts, counts=None, routes=None):
     """``quantized_routes(r, experts, top): ids, active -> counts, routes``.
 

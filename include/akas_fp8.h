@@ -187,6 +187,17 @@ int akas_biased_softmax_router(const float* logits, const float* bias, int32_t* 
                                void* stream);
 
 /*
+ * router(r, experts, top): logits -> ids, weights (the block-fp8 decode
+ * variant's router kind).
+ * Replaces src/akas/ops/moe/cuda.py:2011-2050 (registered as "router" at
+ * src/akas/ops/moe/definition.py:1651-1657, :1836-1842).  The f32 logits are
+ * rounded to bf16 before selection (ties -> lowest index); weights = softmax
+ * over the selected rounded logits, relative to the first (largest) one.
+ */
+int akas_router(const float* logits, int32_t* ids, float* weights, int64_t r, int experts,
+                int top, void* stream);
+
+/*
  * quantized_routes(r, experts, top): ids, active -> counts, routes.
  * Replaces src/akas/ops/moe/kernel.py:121-151 and the parallel variant
  * src/akas/ops/moe/cuda.py:2187-2322.  Stable (row, rank) order, bit-exact;

@@ -68,6 +68,18 @@ def biased_softmax_router(logits, bias, top, scale=1.0):
     return ids, p.astype(np.float32)
 
 
+def router(logits, top):
+    """The block-fp8 decode variant's router (``src/akas/ops/moe/cuda.py:2011-2050``):
+    the f32 logits are rounded to bf16, selected by repeated maximum (ties ->
+    lowest index) and weighted ``exp(l_j - l_0) / sum_rank exp(l_rank - l_0)``
+    over the selected rounded logits, ``l_0`` the first (largest) one."""
+    values = bf16_round(np.asarray(logits, np.float32))
+    ids = _iterative_topk(values, top)
+    selected = np.take_along_axis(values.astype(np.float64), ids, axis=1)
+    p = np.exp(selected - selected[:, :1])
+    return ids, (p / p.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
 # --------------------------------------------------------------------------
 # routes, tile maps, packing
 # --------------------------------------------------------------------------
@@ -392,8 +404,7 @@ def shared_expert_moe_layer(x, logits, shared_gate, w1, s1, w3, s3, w2, s2,
     with the shared expert's sigmoid gate.  Returns float32 ``[T, H]``."""
     x = np.asarray(x, np.float32)
     T = x.shape[0]
-    logits = bf16_round(np.asarray(logits, np.float32))
-    ids, prob = biased_softmax_router(logits, np.zeros(logits.shape[1], np.float32), top)
+    ids, prob = router(logits, top)
     source = fake_quantize(x).astype(np.float64)
     contributions = np.zeros((T, top, w2.shape[1]), np.float32)
     for e in range(w1.shape[0]):

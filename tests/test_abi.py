@@ -59,6 +59,12 @@ def test_host_validation_rejects_before_launch():
     assert lib.akas_expert_tile_map(1, 1, 1, 4, 8, 2, 48, None) == -1
     # router: top larger than experts
     assert lib.akas_biased_router(1, 1, 1, 1, 4, 8, 9, 1.0, 1, None) == -1
+    # block-fp8 router: top above 32 or experts, experts above 1024, nulls, no rows
+    assert lib.akas_router(1, 1, 1, 4, 64, 33, None) == -1
+    assert lib.akas_router(1, 1, 1, 4, 8, 9, None) == -1
+    assert lib.akas_router(1, 1, 1, 4, 1025, 4, None) == -1
+    assert lib.akas_router(None, 1, 1, 4, 64, 4, None) == -2
+    assert lib.akas_router(None, None, None, 0, 64, 4, None) == 0
     # expert partial: o not a multiple of 128
     assert lib.akas_expert_partial(1, 1, 1, 1, 0, 1, 1, 1, 1, None, 1, 0, 4, 2, 4, 100, 256,
                                    0, 1, 64, 0, None) == -1

@@ -40,11 +40,13 @@ def pattern_routes(rows, top, experts, mult=1, inactive_last=True):
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("rows,experts,top", [(1, 64, 4), (257, 64, 4), (64, 256, 8), (9, 7, 3),
-                                              (1000, 64, 8), (33, 32, 6), (17, 64, 1)])
+                                              (1000, 64, 8), (33, 32, 6), (17, 64, 1),
+                                              (20, 1000, 6)])
 def test_softmax_router(dev, rows, experts, top):
     """Up to 64 experts and top 8 take the sixteen-lanes-per-row kernel, the
-    rest the one-wave-per-row kernel; ties within a lane's experts (0, 1) and
-    across lanes (20, 40) resolve to the lower id."""
+    rest the one-wave-per-row kernel (4 expert slots per lane up to 256
+    experts, 16 above); ties within a lane's experts (0, 1) and across lanes
+    (20, 40) resolve to the lower id."""
     from akas_amd import ops
 
     rng = np.random.default_rng(17)
@@ -58,6 +60,28 @@ def test_softmax_router(dev, rows, experts, top):
     ids, w = ops.biased_softmax_router(_t(logits, dev), _t(bias, dev), top=top, scale=1.5)
     eids, ew = omoe.biased_softmax_router(logits, bias, top, scale=1.5)
     np.testing.assert_array_equal(_np(ids), eids)
+    np.testing.assert_allclose(_np(w), ew, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("rows,experts,top", [(64, 256, 8), (257, 64, 4), (3, 300, 5), (9, 7, 3),
+                                              (1, 64, 8)])
+def test_decode_router(dev, rows, experts, top):
+    """The block-fp8 router kind: selection on the bf16-rounded logits.  Row 0
+    holds 1 and 1 + 2^-10 (one bf16 value) as its two largest logits, the
+    larger f32 value at the higher index: the tie goes to the lower index.
+    Covers the sixteen-lanes-per-row kernel (<= 64 experts) and the
+    one-wave-per-row kernel with 4 (<= 256) and 16 expert slots per lane."""
+    from akas_amd import ops
+
+    rng = np.random.default_rng(19)
+    logits = rng.normal(0, 1, (rows, experts)).astype(np.float32)
+    logits[0] = np.minimum(logits[0], 0.5)
+    logits[0, 1] = 1.0
+    logits[0, min(5, experts - 1)] = np.float32(1.0 + 2.0 ** -10)
+    ids, w = ops.router(_t(logits, dev), top=top)
+    eids, ew = omoe.router(logits, top)
+    np.testing.assert_array_equal(_np(ids), eids)
+    assert _np(ids)[0, 0] == 1
     np.testing.assert_allclose(_np(w), ew, rtol=2e-6, atol=1e-7)
 
 

@@ -52,6 +52,37 @@ def test_softmax_router(rows, experts, top):
     np.testing.assert_array_equal(zero_ids[0], np.arange(top))
 
 
+def _bf16_tie_logits(rng, rows, experts):
+    """Random logits with, in row 0, two distinct f32 values that round to the
+    same bf16 value (1 and 1 + 2^-10), the larger one at the higher index, as
+    the row's two largest logits."""
+    logits = rng.normal(0, 1, (rows, experts)).astype(np.float32)
+    logits[0] = np.minimum(logits[0], 0.5)
+    lo, hi = 1, min(5, experts - 1)
+    logits[0, lo] = 1.0
+    logits[0, hi] = np.float32(1.0 + 2.0 ** -10)
+    return logits
+
+
+@pytest.mark.parametrize("rows,experts,top", [(40, 64, 4), (9, 7, 3), (5, 256, 8)])
+def test_decode_router(rows, experts, top):
+    """Closed forms: stable argsort of the bf16-rounded logits (rounded by
+    torch, not the oracle's own rounding) and scipy's softmax over the
+    selected ones; the bf16 tie in row 0 goes to the lower index although the
+    f32 logit at the higher index is larger."""
+    import torch
+
+    rng = np.random.default_rng(23)
+    logits = _bf16_tie_logits(rng, rows, experts)
+    ids, w = omoe.router(logits, top)
+    rounded = torch.from_numpy(logits).to(torch.bfloat16).float().numpy()
+    exp_ids = np.argsort(-rounded, axis=1, kind="stable")[:, :top]
+    np.testing.assert_array_equal(ids, exp_ids)
+    assert ids[0, 0] == 1 and (top < 2 or ids[0, 1] == min(5, experts - 1))
+    sel = np.take_along_axis(rounded.astype(np.float64), exp_ids, axis=1)
+    np.testing.assert_allclose(w, softmax(sel, axis=1), rtol=1e-6)
+
+
 @pytest.mark.parametrize("normalize", [True, False])
 def test_sigmoid_router(normalize):
     rng = np.random.default_rng(22)
