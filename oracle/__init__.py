@@ -27,7 +27,8 @@ Pinning (what each function is checked against, in ``tests/test_oracle_*.py``):
   float64 result is exact, linearity in the weight scales, and a per-element
   brute-force triple loop on tiny shapes.
 * routing, tile maps and packing: brute-force enumerations written
-  independently in the tests (stable argsort, explicit loops), the
+  independently in the tests (stable argsort, explicit loops; the block-fp8
+  ``router`` against stable argsort of torch-rounded bf16 logits), the
   deterministic route patterns of ``src/akas/ops/moe/validation.py:82-99`` and
   ``:606-611``, and the empty-batch invariants of ``tests/test_lfm_moe.py``.
 * ``routed_combine``: explicit per-element loop.
