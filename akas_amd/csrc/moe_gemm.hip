@@ -455,6 +455,53 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
 }
 
 // ---------------------------------------------------------------------------
+// fp8_experts' group tables (moe_groups: experts [r*top], routes [r*top, r]
+// holding a rank or -1) -> the grouped kernels' per-expert counts and routes
+// (row*top + rank, in row order).  One workgroup per expert finds the group
+// that owns it (each expert has at most one) and compacts that group's route
+// row by an ordered block scan; an expert no group owns gets count 0.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void groups_to_routes_kernel(const int32_t* __restrict__ group_experts,
+                                                               const int32_t* __restrict__ group_routes,
+                                                               int32_t* __restrict__ counts,
+                                                               int32_t* __restrict__ routes,
+                                                               int64_t rows, int top) {
+  __shared__ int owner;
+  __shared__ int wave_tot[4];
+  const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) owner = 0x7FFFFFFF;
+  __syncthreads();
+  const int64_t groups = rows * top;
+  for (int64_t g = tid; g < groups; g += 256)
+    if (group_experts[g] == e) atomicMin(&owner, (int)g);
+  __syncthreads();
+  const int g = owner;  // uniform
+  int32_t* out = routes + (int64_t)e * rows;
+  int64_t base = 0;
+  if (g != 0x7FFFFFFF) {
+    const int32_t* row = group_routes + (int64_t)g * rows;
+    for (int64_t b0 = 0; b0 < rows; b0 += 256) {
+      const int64_t b = b0 + tid;
+      const int rank = b < rows ? row[b] : -1;
+      const int live = rank >= 0 && rank < top;
+      const int incl = wave_inclusive_scan(live, lane);
+      if (lane == 63) wave_tot[wave] = incl;
+      __syncthreads();
+      int before = 0, total = 0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        before += w < wave ? wave_tot[w] : 0;
+        total += wave_tot[w];
+      }
+      if (live) out[base + before + incl - 1] = (int32_t)(b * top + rank);
+      base += total;
+      __syncthreads();
+    }
+  }
+  if (tid == 0) counts[e] = (int32_t)base;
+}
+
+// ---------------------------------------------------------------------------
 // launch
 // ---------------------------------------------------------------------------
 
@@ -614,6 +661,67 @@ extern "C" int akas_fp8_expert_swiglu(const uint8_t* x, const float* activation_
   a.parts = 1; a.kb_per_part = (int)(k / kBlock);
   a.ws_dtype = scale_dtype; a.prod_dtype = product_dtype; a.act_dtype = activation_dtype;
   launch_swiglu(a, reinterpret_cast<hipStream_t>(stream));
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+// fp8_experts workspace: row-major codes and scales of the quantized input,
+// then the per-expert counts and routes built from the group tables.
+static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static int64_t fp8_experts_rows(int64_t r, int top, int routed_input) {
+  return routed_input ? r * top : r;
+}
+
+extern "C" size_t akas_fp8_experts_workspace_size(int64_t r, int top, int experts, int64_t k,
+                                                  int routed_input) {
+  if (r <= 0 || top < 1 || experts < 1 || k <= 0) return 0;
+  const int64_t rows = fp8_experts_rows(r, top, routed_input);
+  return align256((size_t)(rows * k)) + align256((size_t)(rows * (k / kBlock)) * sizeof(float)) +
+         align256((size_t)experts * sizeof(int32_t)) + (size_t)experts * (size_t)r * sizeof(int32_t);
+}
+
+extern "C" int akas_fp8_experts(const void* x, int x_dtype, const uint8_t* w, const void* w_scales,
+                                int scale_dtype, const int32_t* group_experts,
+                                const int32_t* group_routes, void* out, int out_dtype,
+                                void* workspace, size_t workspace_bytes, int64_t r, int top,
+                                int experts, int64_t o, int64_t k, int routed_input,
+                                void* stream) {
+  const int64_t rows = r < 0 || top < 1 ? 0 : fp8_experts_rows(r, top, routed_input);
+  int st = check_common(r, top, experts, o, k, 64, 0, rows);
+  if (st != AKAS_OK) return st;
+  if (r * top > 0x7FFFFFFF || (uint64_t)experts * (uint64_t)r >= (1ull << 31))
+    return AKAS_ERR_GEOMETRY;
+  if (!float_dtype(x_dtype) || !float_dtype(out_dtype) || !scale_dtype_ok(scale_dtype))
+    return AKAS_ERR_DTYPE;
+  if (r == 0) return AKAS_OK;
+  if (!x || !w || !w_scales || !group_experts || !group_routes || !out) return AKAS_ERR_NULL;
+  if (!workspace || workspace_bytes < akas_fp8_experts_workspace_size(r, top, experts, k, routed_input))
+    return AKAS_ERR_WORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  uint8_t* codes = reinterpret_cast<uint8_t*>(workspace);
+  float* scales = reinterpret_cast<float*>(codes + align256((size_t)(rows * k)));
+  int32_t* counts = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(scales) +
+                                               align256((size_t)(rows * (k / kBlock)) * sizeof(float)));
+  int32_t* routes = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(counts) +
+                                               align256((size_t)experts * sizeof(int32_t)));
+  st = launch_quantize(x, x_dtype, codes, scales, rows, k, false, s);
+  if (st != AKAS_OK) return st;
+  groups_to_routes_kernel<<<experts, 256, 0, s>>>(group_experts, group_routes, counts, routes, r,
+                                                  top);
+  ExpertArgs a{};
+  a.x = codes; a.as = scales; a.w = w; a.ws = w_scales;
+  a.counts = counts; a.routes = routes; a.out = out;
+  a.r = (int)r; a.top = top; a.E = experts; a.N = (int)o; a.K = (int)k;
+  a.routed = routed_input; a.packed_in = 0; a.packed_out = 0;
+  a.x_rows = (int)rows; a.out_rows = (int)(r * top);
+  a.parts = 1; a.kb_per_part = (int)(k / kBlock);
+  a.ws_dtype = scale_dtype;
+  switch (out_dtype) {
+    case AKAS_DTYPE_F32: launch_partial<AKAS_DTYPE_F32>(a, s); break;
+    case AKAS_DTYPE_BF16: launch_partial<AKAS_DTYPE_BF16>(a, s); break;
+    default: launch_partial<AKAS_DTYPE_F16>(a, s);
+  }
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }

@@ -367,6 +367,33 @@ __global__ __launch_bounds__(1024) void routes4_kernel(const int32_t* __restrict
 }
 
 // ---------------------------------------------------------------------------
+// moe_groups (src/akas/ops/moe/cuda.py:1978-2008), the block-fp8 decode
+// variant's route tables: one workgroup per (row, rank) group g of the
+// flattened ids.  g owns its expert when no earlier group holds it; the owner
+// records the expert and, for every row b, the rank at which b selected it
+// (the last such rank), -1 elsewhere; every other group records -1s.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void moe_groups_kernel(const int32_t* __restrict__ ids,
+                                                         int32_t* __restrict__ experts,
+                                                         int32_t* __restrict__ routes,
+                                                         int64_t rows, int top) {
+  const int64_t g = blockIdx.x;
+  const int expert = ids[g];
+  int earlier = 0;
+  for (int64_t e = threadIdx.x; e < g; e += 256) earlier |= ids[e] == expert;
+  const bool owner = !__syncthreads_or(earlier);
+  if (threadIdx.x == 0) experts[g] = owner ? expert : -1;
+  int32_t* out = routes + g * rows;
+  for (int64_t b = threadIdx.x; b < rows; b += 256) {
+    int rank = -1;
+    if (owner)
+      for (int j = 0; j < top; ++j)
+        if (ids[b * top + j] == expert) rank = j;
+    out[b] = rank;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // per-expert tile prefix (shared by the tile map and the pack kernel)
 // ---------------------------------------------------------------------------
 
@@ -678,6 +705,17 @@ extern "C" int akas_quantized_routes(const int32_t* ids, const int32_t* active, 
     routes4_kernel<<<experts, 1024, 0, s>>>(ids, active, counts, routes, r);
   else
     routes_kernel<<<experts, 1024, 0, s>>>(ids, active, counts, routes, r, top);
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_moe_groups(const int32_t* ids, int32_t* experts, int32_t* routes, int64_t r,
+                               int top, void* stream) {
+  if (r < 0 || top < 1 || r * top > 0x7FFFFFFF) return AKAS_ERR_GEOMETRY;
+  if (r == 0) return AKAS_OK;
+  if (!ids || !experts || !routes) return AKAS_ERR_NULL;
+  moe_groups_kernel<<<(int)(r * top), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      ids, experts, routes, r, top);
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }

@@ -147,9 +147,28 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
     return out
 
 
+def _group_contributions(x, ids, weights: ExpertWeights, *, top):
+    """The routed experts exactly as the block-fp8 decode program emits them
+    (src/akas/ops/moe/definition.py:306-343): ``moe_groups`` tables,
+    ``fp8_experts`` for gate and up, ``swiglu_experts`` and ``fp8_experts``
+    for the down projection on the routed activations -> f32 ``[T, top, H]``."""
+    rows = x.shape[0]
+    experts, routes = ops.moe_groups(ids)
+    shape = (rows, top, weights.width)
+    g = ops.fp8_experts(x, weights.w1, weights.s1, experts, routes, top=top,
+                        out=torch.empty(shape, dtype=torch.float32, device=x.device))
+    u = ops.fp8_experts(x, weights.w3, weights.s3, experts, routes, top=top,
+                        out=torch.empty(shape, dtype=torch.float32, device=x.device))
+    activated = ops.swiglu_experts(g, u)
+    return ops.fp8_experts(activated, weights.w2, weights.s2, experts, routes, top=top,
+                           routed_input=True,
+                           out=torch.empty((rows, top, x.shape[1]), dtype=torch.float32,
+                                           device=x.device))
+
+
 def shared_expert_moe(x, logits, shared_gate, weights: ExpertWeights, shared: SharedExpert, *,
                       top, fused_swiglu=True, packed=False, max_block_m=64,
-                      contribution_dtype=torch.bfloat16):
+                      contribution_dtype=torch.bfloat16, routed_kinds="routes"):
     """The Qwen3.5 block-fp8 MoE block: ``x [T, H]``, router ``logits [T, E]``
     and the shared expert's gate logit ``shared_gate [T]`` (both from the
     caller's bf16 projections) -> f32 ``[T, H]``.
@@ -162,13 +181,24 @@ def shared_expert_moe(x, logits, shared_gate, weights: ExpertWeights, shared: Sh
     combine adds it under its sigmoid gate (``moe_combine``,
     src/akas/ops/moe/cuda.py:392-422).  ``contribution_dtype`` bf16 loses
     nothing: the combine rounds each contribution to bf16 first.
+
+    ``routed_kinds="groups"`` runs the routed experts through the decode
+    program's own kinds (``moe_groups`` -> ``fp8_experts`` x2 ->
+    ``swiglu_experts`` -> ``fp8_experts``); the default ``"routes"`` uses
+    ``quantized_routes`` and the grouped GEMMs above (one fused gate/up
+    launch).
     """
     rows = x.shape[0]
     ids, probability = ops.router(logits, top=top)
-    contributions, _, _ = _expert_contributions(
-        x, ids, _all_active(rows, x.device), weights, top=top, fused_swiglu=fused_swiglu,
-        packed=packed, max_block_m=max_block_m, product_dtype=torch.float32,
-        activation_dtype=torch.float32, contribution_dtype=contribution_dtype)
+    if routed_kinds == "groups":
+        contributions = _group_contributions(x, ids, weights, top=top)
+    elif routed_kinds == "routes":
+        contributions, _, _ = _expert_contributions(
+            x, ids, _all_active(rows, x.device), weights, top=top, fused_swiglu=fused_swiglu,
+            packed=packed, max_block_m=max_block_m, product_dtype=torch.float32,
+            activation_dtype=torch.float32, contribution_dtype=contribution_dtype)
+    else:
+        raise ValueError(f"unknown routed_kinds {routed_kinds!r}")
     width = shared.w1.shape[0]
     g = ops.fp8_linear(x, shared.w1, shared.s1)
     u = ops.fp8_linear(x, shared.w3, shared.s3)

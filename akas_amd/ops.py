@@ -297,6 +297,20 @@ def router(logits, *, top, ids=None, weights=None):
     return ids, weights
 
 
+def moe_groups(ids, *, experts=None, routes=None):
+    """``moe_groups(r, top): ids -> experts, routes``, the block-fp8 decode
+    variant's route tables (src/akas/ops/moe/cuda.py:1978-2008): per (row,
+    rank) group the expert it owns (first occurrence) or -1, and per owning
+    group the rank at which each row selected it, or -1."""
+    _need(ids, "ids", torch.int32)
+    r, top = ids.shape
+    experts = _out(experts, "experts", (r * top,), torch.int32, ids)
+    routes = _out(routes, "routes", (r * top, r), torch.int32, ids)
+    check(_lib.load().akas_moe_groups(_ptr(ids), _ptr(experts), _ptr(routes), r, top,
+                                      _stream()), "moe_groups")
+    return experts, routes
+
+
 def quantized_routes(ids, active, *, experts, counts=None, routes=None):
     """``quantized_routes(r, experts, top): ids, active -> counts, routes``.
 
@@ -413,6 +427,49 @@ def expert_partial(x, activation_scales, w, scales, counts, routes, tile_experts
         _ptr(routes), _ptr(tile_experts), _ptr(tile_offsets), _ptr(expert_offsets), _ptr(out),
         _dt(out.dtype), r, top, experts, o, k, int(bool(routed_input)), partitions, max_block_m,
         int(bool(packed_input)), _stream()), "expert_partial")
+    return out
+
+
+def fp8_experts_workspace(r, top, experts, k, routed_input, device):
+    """Workspace of :func:`fp8_experts` (quantized input and the per-expert
+    route tables built from the group tables)."""
+    n = _lib.load().akas_fp8_experts_workspace_size(r, top, experts, k, int(bool(routed_input)))
+    return torch.empty(max(int(n), 1), dtype=torch.uint8, device=device)
+
+
+def fp8_experts(x, w, scales, experts, routes, *, top, routed_input=False, out=None,
+                output_dtype=torch.float32, workspace=None):
+    """``fp8_experts(r, experts, top, o, k, routed_input)``: the block-fp8
+    decode variant's expert products over moe_groups' tables
+    (src/akas/ops/moe/cuda.py:439-531).
+
+    ``x`` f32/f16/bf16 ``[r, k]`` (``[r, top, k]`` routed) is quantized per
+    1x128 group; ``out[b, rank] = x_row . dequant(w[e])^T`` for every group of
+    expert ``e`` and row ``b`` it routes; ``out`` ``[r, top, o]`` entries that
+    no group routes are left as they are.
+    """
+    _need(x, "x", _FLOATS)
+    _need(w, "w", torch.uint8)
+    num_experts, o, k = w.shape
+    r = x.shape[0]
+    if routed_input and (x.dim() != 3 or x.shape[1] != top):
+        raise ValueError("routed fp8_experts input must be [r, top, k]")
+    if not routed_input and x.dim() != 2:
+        raise ValueError("fp8_experts input must be [r, k]")
+    if x.shape[-1] != k:
+        raise ValueError("x and w disagree on k")
+    _need(scales, "scales", _SCALES, (num_experts, (o + BLOCK - 1) // BLOCK, k // BLOCK))
+    _need(experts, "experts", torch.int32, (r * top,))
+    _need(routes, "routes", torch.int32, (r * top, r))
+    if out is None:
+        out = torch.zeros((r, top, o), dtype=output_dtype, device=x.device)
+    _need(out, "out", _FLOATS, (r, top, o))
+    if workspace is None:
+        workspace = fp8_experts_workspace(r, top, num_experts, k, routed_input, x.device)
+    check(_lib.load().akas_fp8_experts(
+        _ptr(x), _dt(x.dtype), _ptr(w), _ptr(scales), _dt(scales.dtype), _ptr(experts),
+        _ptr(routes), _ptr(out), _dt(out.dtype), _ptr(workspace), workspace.numel(), r, top,
+        num_experts, o, k, int(bool(routed_input)), _stream()), "fp8_experts")
     return out
 
 

@@ -198,6 +198,17 @@ int akas_router(const float* logits, int32_t* ids, float* weights, int64_t r, in
                 int top, void* stream);
 
 /*
+ * moe_groups(r, top): ids -> experts, routes (the block-fp8 decode variant's
+ * route tables).  Replaces src/akas/ops/moe/cuda.py:1978-2008.  For each
+ * (row, rank) group g of ids [r, top]: experts[g] = ids[g] when no earlier
+ * group (in row, rank order) holds that expert, else -1; routes [r*top, r]:
+ * for an owning group, routes[g, b] = the last rank at which row b selected
+ * the expert, or -1; all -1 for other groups.  Bit-exact.
+ */
+int akas_moe_groups(const int32_t* ids, int32_t* experts, int32_t* routes, int64_t r, int top,
+                    void* stream);
+
+/*
  * quantized_routes(r, experts, top): ids, active -> counts, routes.
  * Replaces src/akas/ops/moe/kernel.py:121-151 and the parallel variant
  * src/akas/ops/moe/cuda.py:2187-2322.  Stable (row, rank) order, bit-exact;
@@ -258,6 +269,24 @@ int akas_expert_partial(const uint8_t* x, const float* activation_scales, const 
                         int out_dtype, int64_t r, int top, int experts, int64_t o, int64_t k,
                         int routed_input, int partitions, int max_block_m, int packed_input,
                         void* stream);
+
+/*
+ * fp8_experts(r, experts, top, o, k, routed_input): x, w, scales, experts,
+ * routes -> out (the block-fp8 decode variant's expert products).
+ * Replaces src/akas/ops/moe/cuda.py:439-531.  x f32/f16/bf16 [r, k] (or
+ * [r, top, k] when routed_input) is quantized per 1x128 group; for every
+ * group g with experts[g] = e >= 0 and row b with rank = routes[g, b] >= 0,
+ * out[b, rank, :] = x_row . dequant(w[e])^T with x_row = x[b] (x[b, rank]
+ * when routed), f32 accumulation; other entries of out are left untouched.
+ * The group tables are moe_groups'.  o % 128 == 0 and k % 128 == 0; the
+ * caller's workspace holds at least akas_fp8_experts_workspace_size() bytes.
+ */
+size_t akas_fp8_experts_workspace_size(int64_t r, int top, int experts, int64_t k,
+                                       int routed_input);
+int akas_fp8_experts(const void* x, int x_dtype, const uint8_t* w, const void* w_scales,
+                     int scale_dtype, const int32_t* group_experts, const int32_t* group_routes,
+                     void* out, int out_dtype, void* workspace, size_t workspace_bytes, int64_t r,
+                     int top, int experts, int64_t o, int64_t k, int routed_input, void* stream);
 
 /*
  * fp8_expert_swiglu(r, top, experts, o, k[, product_dtype, activation_dtype,

@@ -107,6 +107,59 @@ def quantized_routes(ids, active, experts):
     return counts, routes
 
 
+def moe_groups(ids):
+    """The block-fp8 decode variant's route tables
+    (``src/akas/ops/moe/cuda.py:1978-2008``).
+
+    Over the flattened ``(row, rank)`` groups ``g`` of ``ids [r, top]``:
+    ``experts[g] = ids[g]`` when no earlier group holds that expert, else -1;
+    ``routes[g, b]`` = the last rank ``j`` with ``ids[b, j] == experts[g]`` for
+    an owning group (-1 when row ``b`` did not select it), all -1 otherwise.
+    """
+    ids = np.asarray(ids, np.int32)
+    r, top = ids.shape
+    flat = ids.reshape(-1)
+    experts = np.full(r * top, -1, np.int32)
+    routes = np.full((r * top, r), -1, np.int32)
+    seen = set()
+    for g, e in enumerate(flat.tolist()):
+        if e in seen:
+            continue
+        seen.add(e)
+        experts[g] = e
+        for b in range(r):
+            for j in range(top):
+                if ids[b, j] == e:
+                    routes[g, b] = j
+    return experts, routes
+
+
+def fp8_experts(x, w, scales, experts, routes, top, routed_input=False, out=None):
+    """The block-fp8 decode variant's expert products over moe_groups' tables
+    (``src/akas/ops/moe/cuda.py:439-531``): each routed row of ``x`` (float,
+    ``[r, k]`` or ``[r, top, k]``) is quantized per 1x128 group and
+    multiplied by the dequantized ``w[e]`` in float64;
+    ``out[b, rank] = x_row . w[e]^T`` for group ``g`` of expert ``e`` and
+    ``rank = routes[g, b] >= 0``.  Other entries keep ``out``'s values."""
+    x = np.asarray(x, np.float32)
+    r, k = x.shape[0], x.shape[-1]
+    E, o, _ = w.shape
+    out = np.zeros((r, top, o), np.float32) if out is None else np.array(out, np.float32)
+    source = fake_quantize(x.reshape(-1, k)).reshape(x.shape).astype(np.float64)
+    for g in range(r * top):
+        e = int(experts[g])
+        if e < 0 or e >= E:
+            continue
+        weight = dequantize_weight(w[e], scales[e])
+        for b in range(r):
+            rank = int(routes[g, b])
+            if rank < 0 or rank >= top:
+                continue
+            row = source[b, rank] if routed_input else source[b]
+            out[b, rank] = (row @ weight.T).astype(np.float32)
+    return out
+
+
 def tile_capacity(rows, top, experts, block_m):
     """Upper bound of non-empty expert tiles (``src/akas/ops/moe/definition.py:9-16``)."""
     if any(type(v) is not int or v < 1 for v in (rows, top, experts, block_m)):

@@ -65,6 +65,17 @@ def test_host_validation_rejects_before_launch():
     assert lib.akas_router(1, 1, 1, 4, 1025, 4, None) == -1
     assert lib.akas_router(None, 1, 1, 4, 64, 4, None) == -2
     assert lib.akas_router(None, None, None, 0, 64, 4, None) == 0
+    # moe_groups: negative rows, nulls, no rows
+    assert lib.akas_moe_groups(1, 1, 1, -1, 4, None) == -1
+    assert lib.akas_moe_groups(None, 1, 1, 4, 4, None) == -2
+    assert lib.akas_moe_groups(None, None, None, 0, 4, None) == 0
+    # fp8_experts: o not a multiple of 128, x dtype code, nulls, workspace
+    big = 1 << 30
+    assert lib.akas_fp8_experts(1, 2, 1, 1, 0, 1, 1, 1, 0, 1, big, 4, 2, 8, 100, 256, 0, None) == -1
+    assert lib.akas_fp8_experts(1, 7, 1, 1, 0, 1, 1, 1, 0, 1, big, 4, 2, 8, 128, 256, 0, None) == -3
+    assert lib.akas_fp8_experts(1, 2, 1, 1, 0, None, 1, 1, 0, 1, big, 4, 2, 8, 128, 256, 0, None) == -2
+    assert lib.akas_fp8_experts(1, 2, 1, 1, 0, 1, 1, 1, 0, 1, 16, 4, 2, 8, 128, 256, 0, None) == -5
+    assert lib.akas_fp8_experts_workspace_size(4, 2, 8, 256, 1) == 8 * 256 + 256 + 256 + 8 * 4 * 4
     # expert partial: o not a multiple of 128
     assert lib.akas_expert_partial(1, 1, 1, 1, 0, 1, 1, 1, 1, None, 1, 0, 4, 2, 4, 100, 256,
                                    0, 1, 64, 0, None) == -1

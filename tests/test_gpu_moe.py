@@ -625,3 +625,89 @@ def test_shared_expert_moe_block(dev, rows, E, H, F, packed):
     exp = omoe.shared_expert_moe_layer(x, logits, gate, *bank["w1"], *bank["w3"], *bank["w2"],
                                        *bank["sw1"], *bank["sw3"], *bank["sw2"], top)
     assert rel_fro(_np(out), exp) < 1e-2
+
+
+# ---------------------------------------------------------------------------
+# block-fp8 decode variant kinds: moe_groups / fp8_experts
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", ["router64x8", "duplicates", "single", "wide"])
+def test_moe_groups(dev, case):
+    """Bit-exact group tables: distinct top-8 ids over 256 experts, repeated
+    ids inside and across rows (the last rank wins), one id, and 1100 rows
+    (route rows longer than a workgroup's stride)."""
+    from akas_amd import ops
+
+    rng = np.random.default_rng(71)
+    if case == "router64x8":
+        ids = np.argsort(-rng.normal(0, 1, (64, 256)), axis=1, kind="stable")[:, :8]
+    elif case == "duplicates":
+        ids = rng.integers(0, 6, (33, 4))
+        ids[0] = [3, 3, 1, 3]
+    elif case == "single":
+        ids = np.array([[5]])
+    else:
+        ids = rng.integers(0, 40, (1100, 2))
+    ids = ids.astype(np.int32)
+    experts, routes = ops.moe_groups(_t(ids, dev))
+    eexp, eroutes = omoe.moe_groups(ids)
+    np.testing.assert_array_equal(_np(experts), eexp)
+    np.testing.assert_array_equal(_np(routes), eroutes)
+
+
+@pytest.mark.parametrize("r,top,E,o,k,routed,scale_dtype", [
+    (64, 8, 256, 512, 2048, False, "bfloat16"),
+    (64, 8, 256, 2048, 512, True, "bfloat16"),
+    (5, 3, 7, 256, 384, False, "float32"),
+    (300, 4, 16, 128, 256, True, "float32")])
+def test_fp8_experts(dev, r, top, E, o, k, routed, scale_dtype):
+    """The decode variant's expert products over moe_groups' tables: the
+    Qwen3.5 shapes (gate/up o=512 k=2048, down o=2048 k=512 on routed
+    activations) and small ones; rows no group routes keep out's values."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(72 + r)
+    ids = np.stack([rng.permutation(E)[:top] for _ in range(r)]).astype(np.int32)
+    x = bf16_normal(rng, (r, top, k) if routed else (r, k))
+    w = random_codes(rng, (E, o, k))
+    ws = (2.0 ** rng.integers(-8, -4, (E, o // 128, k // 128))).astype(np.float32)
+    if scale_dtype == "bfloat16":
+        ws = ofp8.bf16_round(ws)
+    experts, routes = omoe.moe_groups(ids)
+    experts[experts == ids[0, 0]] = -1  # row 0's first pick routed by no group
+    out = torch.full((r, top, o), 7.0, dtype=torch.float32, device=dev)
+    ops.fp8_experts(_t(x, dev, torch.bfloat16), _t(w, dev), _t(ws, dev, getattr(torch, scale_dtype)),
+                    _t(experts, dev), _t(routes, dev), top=top, routed_input=routed, out=out)
+    exp = omoe.fp8_experts(x, w, ws, experts, routes, top, routed,
+                           out=np.full((r, top, o), 7.0, np.float32))
+    got = _np(out)
+    assert (got[0, 0] == 7.0).all()
+    assert rel_fro(got, exp) < 1e-4  # f32 accumulation, as the grouped products' bar
+
+
+@pytest.mark.parametrize("rows,E,H,F", [(6, 32, 256, 128), (4, 256, 2048, 512)])
+def test_shared_expert_moe_block_group_kinds(dev, rows, E, H, F):
+    """The Qwen3.5 block with its routed experts through the decode program's
+    own kinds (moe_groups, fp8_experts, swiglu_experts) against the block
+    equation and against the routes/grouped-GEMM path."""
+    import torch
+    from akas_amd import moe
+
+    rng = np.random.default_rng(rows * 3 + E)
+    top = 8
+    dbank, bank = _device_bank(dev, rows * 3 + E, {
+        "w1": (E, F, H), "w3": (E, F, H), "w2": (E, H, F),
+        "sw1": (F, H), "sw3": (F, H), "sw2": (H, F)}, 0.02 if H == 2048 else 0.05)
+    x = bf16_normal(rng, (rows, H))
+    logits = rng.normal(0, 1, (rows, E)).astype(np.float32)
+    gate = rng.normal(0, 1.5, rows).astype(np.float32)
+    wts = moe.ExpertWeights(*(a for n in ("w1", "w3", "w2") for a in dbank[n]))
+    shared = moe.SharedExpert(*(a for n in ("sw1", "sw3", "sw2") for a in dbank[n]))
+    args = (_t(x, dev, torch.bfloat16), _t(logits, dev), _t(gate, dev), wts, shared)
+    out = _np(moe.shared_expert_moe(*args, top=top, routed_kinds="groups"))
+    ref_path = _np(moe.shared_expert_moe(*args, top=top))
+    exp = omoe.shared_expert_moe_layer(x, logits, gate, *bank["w1"], *bank["w3"], *bank["w2"],
+                                       *bank["sw1"], *bank["sw3"], *bank["sw2"], top)
+    assert rel_fro(out, exp) < 1e-2
+    assert rel_fro(out, ref_path) < 1e-3

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 from scipy.special import expit, softmax
 
-from golden_inputs import bf16_normal, exact_codes, rel_fro
+from golden_inputs import bf16_normal, exact_codes, random_codes, rel_fro
 from oracle import fp8 as ofp8
 from oracle import moe as omoe
 
@@ -369,3 +369,77 @@ def test_moe_combine_closed_forms():
     got = omoe.moe_combine(e, np.ones((1, 1), np.float32), np.zeros((1, 8), np.float32),
                            np.zeros(1, np.float32))
     assert np.all(got == 1.0)
+
+
+# ---------------------------------------------------------------------------
+# block-fp8 decode variant: moe_groups / fp8_experts
+# ---------------------------------------------------------------------------
+
+def _groups_independent(ids):
+    """moe_groups by a different formulation: owners from np.unique's first
+    indices, ranks from the last matching column of each row."""
+    r, top = ids.shape
+    flat = ids.reshape(-1)
+    _, first = np.unique(flat, return_index=True)
+    experts = np.full(r * top, -1, np.int32)
+    experts[first] = flat[first]
+    routes = np.full((r * top, r), -1, np.int32)
+    for g in first:
+        hit = ids == flat[g]
+        last = top - 1 - np.argmax(hit[:, ::-1], axis=1)
+        routes[g] = np.where(hit.any(axis=1), last, -1)
+    return experts, routes
+
+
+@pytest.mark.parametrize("case", ["router", "duplicates", "single"])
+def test_moe_groups(case):
+    rng = np.random.default_rng(31)
+    if case == "router":
+        ids = np.argsort(-rng.normal(0, 1, (24, 16)), axis=1, kind="stable")[:, :4].astype(np.int32)
+    elif case == "duplicates":
+        ids = rng.integers(0, 5, (9, 3)).astype(np.int32)
+        ids[0] = [2, 2, 2]  # one row selecting an expert three times: the last rank wins
+    else:
+        ids = np.array([[7]], np.int32)
+    experts, routes = omoe.moe_groups(ids)
+    eexp, eroutes = _groups_independent(ids)
+    np.testing.assert_array_equal(experts, eexp)
+    np.testing.assert_array_equal(routes, eroutes)
+    if case == "router":
+        # distinct ids per row: every (row, rank) pair is routed by exactly one owner
+        covered = np.zeros(ids.shape, int)
+        for g in np.nonzero(experts >= 0)[0]:
+            for b in np.nonzero(routes[g] >= 0)[0]:
+                covered[b, routes[g, b]] += 1
+        assert (covered == 1).all()
+    if case == "duplicates":
+        g = int(np.nonzero(experts == 2)[0][0])
+        assert routes[g, 0] == 2
+
+
+@pytest.mark.parametrize("routed_input", [False, True])
+def test_fp8_experts_matches_grouped_products(routed_input):
+    """fp8_experts over moe_groups' tables equals the grouped expert products
+    (pinned separately by exact-product inputs) over quantized_routes' tables
+    for the same ids; entries no group routes keep out's values."""
+    rng = np.random.default_rng(32)
+    r, top, E, o, k = 6, 3, 5, 128, 256
+    ids = np.stack([rng.permutation(E)[:top] for _ in range(r)]).astype(np.int32)
+    x = rng.normal(0, 1, (r, top, k) if routed_input else (r, k)).astype(np.float32)
+    w = random_codes(rng, (E, o, k))
+    ws = (2.0 ** rng.integers(-8, -4, (E, 1, k // 128))).astype(np.float32)
+    experts, routes = omoe.moe_groups(ids)
+    sentinel = np.full((r, top, o), 7.0, np.float32)
+    out = omoe.fp8_experts(x, w, ws, experts, routes, top, routed_input, out=sentinel)
+    counts, proutes = omoe.quantized_routes(ids, np.ones(r, np.int32), E)
+    codes, scales = ofp8.quantize(x.reshape(-1, k))
+    codes = codes.reshape(*x.shape[:-1], k)
+    scales = scales.reshape(*x.shape[:-1], k // 128)
+    exp = omoe.expert_partial(codes, scales, w, ws, counts, proutes, top, routed_input=routed_input,
+                              out=sentinel)
+    np.testing.assert_array_equal(out, exp)
+    # a row that no group routes keeps the sentinel
+    experts2 = experts.copy()
+    experts2[experts2 == ids[0, 0]] = -1
+    out2 = omoe.fp8_experts(x, w, ws, experts2, routes, top, routed_input, out=sentinel)
+    assert (out2[0, 0] == 7.0).all()
