@@ -31,6 +31,11 @@ Pinning (what each function is checked against, in ``tests/test_oracle_*.py``):
   ``router`` against stable argsort of torch-rounded bf16 logits), the
   deterministic route patterns of ``src/akas/ops/moe/validation.py:82-99`` and
   ``:606-611``, and the empty-batch invariants of ``tests/test_lfm_moe.py``.
+* ``moe_groups``: an independent construction (first occurrences from
+  ``np.unique``, ranks from the last matching column) and full coverage of
+  every (row, rank) pair for distinct ids; ``fp8_experts``: equality with
+  the grouped expert products over ``quantized_routes``' tables for the same
+  ids, and untouched entries where no group routes.
 * ``routed_combine``: explicit per-element loop.
 * ``rms_norm`` (``norm.py``): closed forms -- a constant row maps to
   ``sign(c) * w`` as eps -> 0 and to ``c / sqrt(c^2 + eps) * w`` exactly, the
