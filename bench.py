@@ -306,6 +306,18 @@ def rms_quantize_bench(torch, dev, rows=16384, cols=2048, steps=20):
                 frac_hbm=round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
 
 
+def _cpu_model():
+    """The host CPU's model name from /proc/cpuinfo (None where absent)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(budget_s=12.0):
     """The oracle's C restatement of the decode sweep on the host cores."""
     import ctypes
@@ -350,7 +362,7 @@ def cpu_baseline(budget_s=12.0):
         times1.append(time.perf_counter() - t0)
     med1 = float(np.median(times1))
     return dict(value=round(step_bytes / med / 1e9, 2), unit="GB/s", cores=threads,
-                kind="port",
+                kind="port", cpu_model=_cpu_model(), host_cpus=os.cpu_count(),
                 sample=f"full decode sweep (M=1,4,16,64,256; K=2048; N=6144), median of "
                        f"{len(times)} runs, {med * 1e3:.1f} ms/sweep, oracle/cpu_ref.c -O3 "
                        f"-fopenmp f32 accumulation",
