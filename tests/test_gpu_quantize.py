@@ -47,11 +47,24 @@ def test_quantize_stress_and_random(dev, dtype, top):
     assert not c.reshape(-1, 128)[0].any()
 
 
-@pytest.mark.parametrize("shape", [(1, 2048), (16, 2048), (257, 1536), (8192, 2048)])
+@pytest.mark.parametrize("shape", [(1, 2048), (16, 2048), (257, 1536), (8192, 2048),
+                                   (4099, 2048)])
 def test_quantize_large_bit_exact(dev, shape):
+    """4099 rows: a ragged last grid-stride pass."""
     rng = np.random.default_rng(0)
     x = bf16_normal(rng, shape, outliers=0.01)
     c, s, ec, es = _run(x, "bfloat16", dev)
+    np.testing.assert_array_equal(s, es)
+    np.testing.assert_array_equal(c, ec)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16"])
+def test_quantize_large_other_dtypes(dev, dtype):
+    rng = np.random.default_rng(1)
+    x = rng.normal(0, 1, (4100, 2048)).astype(np.float32)
+    if dtype == "float16":
+        x = x.astype(np.float16).astype(np.float32)
+    c, s, ec, es = _run(x, dtype, dev)
     np.testing.assert_array_equal(s, es)
     np.testing.assert_array_equal(c, ec)
 
