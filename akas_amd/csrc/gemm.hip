@@ -824,9 +824,19 @@ static bool dma_fits(const DenseArgs& a, int parts) {
 // tiles, aligned 4-element output vectors and activation-scale vectors,
 // 32-bit code offsets.
 constexpr int kSplitNt = 3;
+// Column tile of the split kernel: 48 columns where N allows; up to 64 rows,
+// narrower tiles for the other multiples of 16, so that small N still
+// spreads over many workgroups (16 columns below 2048 columns, else 32).
+static int split_nt(const DenseArgs& a) {
+  if (a.N % (16 * kSplitNt) == 0) return kSplitNt;
+  if (a.M > 64) return 0;
+  if (a.N % 32 == 0 && a.N >= 2048) return 2;
+  return a.N % 16 == 0 ? 1 : 0;
+}
+
 static bool split_fits(const DenseArgs& a) {
   const int esz = a.out_dtype == AKAS_DTYPE_F32 ? 4 : 2;
-  return a.kb_per_part == kSplitQuarters * kSplitKbw && a.N % (16 * kSplitNt) == 0 &&
+  return a.kb_per_part == kSplitQuarters * kSplitKbw && split_nt(a) > 0 &&
          (int64_t)a.M * a.K < (1ll << 31) && (a.K / kBlock) % 4 == 0 && a.ldo % 4 == 0 &&
          a.part_stride % 4 == 0 && reinterpret_cast<uintptr_t>(a.out) % (4 * esz) == 0 &&
          reinterpret_cast<uintptr_t>(a.as) % 16 == 0;
@@ -836,11 +846,21 @@ static bool split_applies(const DenseArgs& a, int parts) {
   return a.M > 16 && a.M <= 256 && split_fits(a) && parts >= 1;
 }
 
-template <int MT, int PF, int AFIRST, int AF, int OUT, int SDT, int MH = 1>
+template <int MT, int PF, int AFIRST, int AF, int OUT, int SDT, int MH = 1, int NT = kSplitNt>
 static void launch_split(const DenseArgs& a, int parts, hipStream_t s) {
-  const int tiles = ((a.M + 16 * MT * MH - 1) / (16 * MT * MH)) * (a.N / (16 * kSplitNt));
-  dense_split_kernel<MT, kSplitNt, PF, AFIRST, AF, OUT, SDT, MH>
+  const int tiles = ((a.M + 16 * MT * MH - 1) / (16 * MT * MH)) * (a.N / (16 * NT));
+  dense_split_kernel<MT, NT, PF, AFIRST, AF, OUT, SDT, MH>
       <<<dim3(tiles, parts), 64 * kSplitQuarters * MH, 0, s>>>(a);
+}
+
+// Up to 64 rows with the column tile split_nt() picks.
+template <int MT, int AF, int OUT, int SDT>
+static void launch_split_small(const DenseArgs& a, int parts, hipStream_t s) {
+  switch (split_nt(a)) {
+    case 1: launch_split<MT, 4, 1, AF, OUT, SDT, 1, 1>(a, parts, s); break;
+    case 2: launch_split<MT, 4, 1, AF, OUT, SDT, 1, 2>(a, parts, s); break;
+    default: launch_split<MT, 4, 1, AF, OUT, SDT>(a, parts, s);
+  }
 }
 
 // Row tiles of the split kernel by M (16 < M <= 256), two tiles per column
@@ -851,9 +871,9 @@ static void launch_split(const DenseArgs& a, int parts, hipStream_t s) {
 template <int AF, int OUT, int SDT>
 static void launch_split_m(const DenseArgs& a, int parts, hipStream_t s) {
   if (a.M <= 32)
-    launch_split<1, 4, 1, AF, OUT, SDT>(a, parts, s);
+    launch_split_small<1, AF, OUT, SDT>(a, parts, s);
   else if (a.M <= 64)
-    launch_split<2, 4, 1, AF, OUT, SDT>(a, parts, s);
+    launch_split_small<2, AF, OUT, SDT>(a, parts, s);
   else if (a.M <= 128)
     launch_split<2, 2, 0, AF, OUT, SDT, 2>(a, parts, s);
   else

@@ -46,7 +46,10 @@ def test_projection_exact_products(dev, m, k, n):
 # kernel): ragged M, 48-column tiles that straddle 128-column scale blocks
 # (N = 240, 480), and every m-tile height.
 SPLIT_CASES = [(17, 2048, 96), (40, 2048, 480), (64, 2048, 144), (100, 2048, 240),
-               (129, 2048, 192), (256, 2048, 336)]
+               (129, 2048, 192), (256, 2048, 336),
+               # up to 64 rows, N not a multiple of 48: 16-column tiles, and
+               # 32-column tiles from 2048 columns
+               (17, 2048, 16), (40, 2048, 512), (33, 2048, 1040), (64, 2048, 2080)]
 
 
 @pytest.mark.parametrize("m,k,n", SPLIT_CASES)
@@ -92,6 +95,27 @@ def test_fp8_linear_decode_shapes(dev, m, scale_dtype):
     # f32 accumulation; the FP8 MFMA sums each 128-deep block with its own
     # internal precision (~1e-5 relative on random data, exact on exact products)
     assert err < 1e-4, err
+
+
+@pytest.mark.parametrize("m,n", [(64, 512), (20, 1040), (48, 2080)])
+def test_fp8_linear_narrow_tiles_match_two_step(dev, m, n):
+    """Narrow column tiles (N not a multiple of 48, up to 64 rows):
+    fp8_linear's fragment-major path equals quantize -> projection_partial
+    bit for bit, and both match the oracle."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(m + n)
+    codes, scales = block_weights(rng, (n, 2048))
+    x = bf16_normal(rng, (m, 2048), outliers=0.01)
+    xt = _t(x, dev, torch.bfloat16)
+    w, s = _t(codes, dev), _t(scales, dev)
+    y = ops.fp8_linear(xt, w, s, out_dtype=torch.float32)
+    q, qs = ops.quantize(xt)
+    y2 = ops.projection_partial(q, qs, w, s, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), y2.cpu().numpy())
+    assert rel_fro(y.cpu().numpy(), ofp8.fp8_linear(x, codes, scales)) < 1e-4
 
 
 @pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64, 100, 129, 256])
