@@ -824,12 +824,11 @@ static bool dma_fits(const DenseArgs& a, int parts) {
 // tiles, aligned 4-element output vectors and activation-scale vectors,
 // 32-bit code offsets.
 constexpr int kSplitNt = 3;
-// Column tile of the split kernel: 48 columns where N allows; up to 64 rows,
-// narrower tiles for the other multiples of 16, so that small N still
-// spreads over many workgroups (16 columns below 2048 columns, else 32).
+// Column tile of the split kernel: 48 columns where N allows, else narrower
+// tiles for the other multiples of 16, so that small N still spreads over
+// many workgroups (16 columns below 2048 columns, else 32).
 static int split_nt(const DenseArgs& a) {
   if (a.N % (16 * kSplitNt) == 0) return kSplitNt;
-  if (a.M > 64) return 0;
   if (a.N % 32 == 0 && a.N >= 2048) return 2;
   return a.N % 16 == 0 ? 1 : 0;
 }
@@ -853,13 +852,13 @@ static void launch_split(const DenseArgs& a, int parts, hipStream_t s) {
       <<<dim3(tiles, parts), 64 * kSplitQuarters * MH, 0, s>>>(a);
 }
 
-// Up to 64 rows with the column tile split_nt() picks.
-template <int MT, int AF, int OUT, int SDT>
-static void launch_split_small(const DenseArgs& a, int parts, hipStream_t s) {
+// One row-tile configuration with the column tile split_nt() picks.
+template <int MT, int PF, int AFIRST, int AF, int OUT, int SDT, int MH>
+static void launch_split_nt(const DenseArgs& a, int parts, hipStream_t s) {
   switch (split_nt(a)) {
-    case 1: launch_split<MT, 4, 1, AF, OUT, SDT, 1, 1>(a, parts, s); break;
-    case 2: launch_split<MT, 4, 1, AF, OUT, SDT, 1, 2>(a, parts, s); break;
-    default: launch_split<MT, 4, 1, AF, OUT, SDT>(a, parts, s);
+    case 1: launch_split<MT, PF, AFIRST, AF, OUT, SDT, MH, 1>(a, parts, s); break;
+    case 2: launch_split<MT, PF, AFIRST, AF, OUT, SDT, MH, 2>(a, parts, s); break;
+    default: launch_split<MT, PF, AFIRST, AF, OUT, SDT, MH>(a, parts, s);
   }
 }
 
@@ -871,13 +870,13 @@ static void launch_split_small(const DenseArgs& a, int parts, hipStream_t s) {
 template <int AF, int OUT, int SDT>
 static void launch_split_m(const DenseArgs& a, int parts, hipStream_t s) {
   if (a.M <= 32)
-    launch_split_small<1, AF, OUT, SDT>(a, parts, s);
+    launch_split_nt<1, 4, 1, AF, OUT, SDT, 1>(a, parts, s);
   else if (a.M <= 64)
-    launch_split_small<2, AF, OUT, SDT>(a, parts, s);
+    launch_split_nt<2, 4, 1, AF, OUT, SDT, 1>(a, parts, s);
   else if (a.M <= 128)
-    launch_split<2, 2, 0, AF, OUT, SDT, 2>(a, parts, s);
+    launch_split_nt<2, 2, 0, AF, OUT, SDT, 2>(a, parts, s);
   else
-    launch_split<4, 2, 0, AF, OUT, SDT, 2>(a, parts, s);
+    launch_split_nt<4, 2, 0, AF, OUT, SDT, 2>(a, parts, s);
 }
 
 template <int OUT, int SDT>
@@ -1041,11 +1040,21 @@ static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 using namespace akas;
 
+// Deep products at decode-sized batches: 2048-deep partitions of the split
+// kernel with f32 partials, then the serial merge.  0 when not taken.
+constexpr int kSplitDepth = kSplitQuarters * kSplitKbw * kBlock;  // 2048
+static int linear_partitions(int64_t r, int64_t k) {
+  if (r <= kFusedQuantizeRows || r > 256 || k <= kSplitDepth || k % kSplitDepth) return 0;
+  return (int)(k / kSplitDepth);
+}
+
 extern "C" size_t akas_fp8_linear_workspace_size(int64_t r, int64_t k, int64_t o) {
-  (void)o;
   if (r <= 0 || k <= 0) return 0;
   // codes: rows rounded up to the 16-row tiles of the fragment-major layout
-  return align256((size_t)((r + 15) & ~15ll) * k) + align256((size_t)r * (k / kBlock) * sizeof(float));
+  size_t n = align256((size_t)((r + 15) & ~15ll) * k) + align256((size_t)r * (k / kBlock) * sizeof(float));
+  const int parts = linear_partitions(r, k);
+  if (parts > 0 && o > 0) n += (size_t)r * parts * o * sizeof(float);  // f32 partials
+  return n;
 }
 
 extern "C" int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const void* w_scales,
@@ -1071,6 +1080,25 @@ extern "C" int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, con
   }
   uint8_t* codes = reinterpret_cast<uint8_t*>(workspace);
   float* scales = reinterpret_cast<float*>(codes + align256((size_t)((r + 15) & ~15ll) * k));
+  const int parts = linear_partitions(r, k);
+  if (parts > 0) {
+    float* partial = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(scales) +
+                                              align256((size_t)r * (k / kBlock) * sizeof(float)));
+    DenseArgs p{codes, scales, w, w_scales, partial, (int64_t)parts * o, o, (int)r, (int)o,
+                (int)k, (int)(k / kBlock / parts), scale_dtype, AKAS_DTYPE_F32, nullptr, 0};
+    if (split_applies(p, parts)) {
+      const int st = launch_quantize(x, x_dtype, codes, scales, r, k, true, s);
+      if (st != AKAS_OK) return st;
+      if (scale_dtype == AKAS_DTYPE_F32)
+        launch_split_m<1, AKAS_DTYPE_F32, AKAS_DTYPE_F32>(p, parts, s);
+      else
+        launch_split_m<1, AKAS_DTYPE_F32, AKAS_DTYPE_BF16>(p, parts, s);
+      const int64_t n = r * o, want = (n + 255) / 256;
+      merge_kernel<<<(int)(want < 16384 ? want : 16384), 256, 0, s>>>(partial, out, out_dtype, r, o,
+                                                                       parts);
+      return hipGetLastError() == hipSuccess ? AKAS_OK : AKAS_ERR_LAUNCH;
+    }
+  }
   DenseArgs a{codes, scales, w, w_scales, out, o, 0, (int)r, (int)o, (int)k,
               (int)(k / kBlock), scale_dtype, out_dtype, nullptr, 0};
   const bool frag = split_applies(a, 1);

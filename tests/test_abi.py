@@ -90,3 +90,6 @@ def test_workspace_size_formula():
     assert lib.akas_fp8_linear_workspace_size(0, 2048, 6144) == 0
     # codes take whole 16-row tiles (the decode GEMM's fragment-major layout)
     assert lib.akas_fp8_linear_workspace_size(17, 2048, 6144) == 32 * 2048 + 17 * 16 * 4 + 192
+    # deeper than 2048 at 17-256 rows: f32 partials of the 2048-deep partitions
+    assert lib.akas_fp8_linear_workspace_size(64, 8192, 2048) == 64 * 8192 + 64 * 64 * 4 + 64 * 4 * 2048 * 4
+    assert lib.akas_fp8_linear_workspace_size(16, 8192, 2048) == 16 * 8192 + 16 * 64 * 4

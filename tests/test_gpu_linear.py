@@ -47,9 +47,10 @@ def test_projection_exact_products(dev, m, k, n):
 # (N = 240, 480), and every m-tile height.
 SPLIT_CASES = [(17, 2048, 96), (40, 2048, 480), (64, 2048, 144), (100, 2048, 240),
                (129, 2048, 192), (256, 2048, 336),
-               # up to 64 rows, N not a multiple of 48: 16-column tiles, and
-               # 32-column tiles from 2048 columns
-               (17, 2048, 16), (40, 2048, 512), (33, 2048, 1040), (64, 2048, 2080)]
+               # N not a multiple of 48: 16-column tiles, and 32-column tiles
+               # from 2048 columns, for four- and eight-wave row tiles
+               (17, 2048, 16), (40, 2048, 512), (33, 2048, 1040), (64, 2048, 2080),
+               (100, 2048, 2080), (200, 2048, 1040), (256, 2048, 16)]
 
 
 @pytest.mark.parametrize("m,k,n", SPLIT_CASES)
@@ -113,6 +114,30 @@ def test_fp8_linear_narrow_tiles_match_two_step(dev, m, n):
     y = ops.fp8_linear(xt, w, s, out_dtype=torch.float32)
     q, qs = ops.quantize(xt)
     y2 = ops.projection_partial(q, qs, w, s, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), y2.cpu().numpy())
+    assert rel_fro(y.cpu().numpy(), ofp8.fp8_linear(x, codes, scales)) < 1e-4
+
+
+@pytest.mark.parametrize("m,k,n", [(64, 8192, 2048), (17, 4096, 512), (40, 4096, 1040),
+                                   (256, 4096, 6144), (100, 6144, 480), (128, 8192, 2048)])
+def test_fp8_linear_deep_k_partitions(dev, m, k, n):
+    """Deeper than 2048 at 17-256 rows: fp8_linear runs 2048-deep partitions
+    with f32 partials and the serial merge -- bit for bit the
+    projection_partial(partitions) -> projection_merge pair on the same codes
+    -- and matches the oracle."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(m + k + n)
+    codes, scales = block_weights(rng, (n, k))
+    x = bf16_normal(rng, (m, k), outliers=0.01)
+    xt = _t(x, dev, torch.bfloat16)
+    w, s = _t(codes, dev), _t(scales, dev)
+    y = ops.fp8_linear(xt, w, s, out_dtype=torch.float32)
+    q, qs = ops.quantize(xt)
+    partial = ops.projection_partial(q, qs, w, s, partitions=k // 2048)
+    y2 = ops.projection_merge(partial, out_dtype=torch.float32)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(y.cpu().numpy(), y2.cpu().numpy())
     assert rel_fro(y.cpu().numpy(), ofp8.fp8_linear(x, codes, scales)) < 1e-4
