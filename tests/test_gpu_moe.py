@@ -711,3 +711,39 @@ def test_shared_expert_moe_block_group_kinds(dev, rows, E, H, F):
                                        *bank["sw1"], *bank["sw3"], *bank["sw2"], top)
     assert rel_fro(out, exp) < 1e-2
     assert rel_fro(out, ref_path) < 1e-3
+
+
+def test_shared_expert_moe_block_graph_replays(dev):
+    """The block forks the shared expert onto a second stream and joins it
+    before the combine; captured in a HIP graph, every replay (with eager work
+    and synchronizations between them) equals the eager result."""
+    import torch
+    from akas_amd import moe
+
+    rows, E, H, F, top = 6, 32, 256, 128, 8
+    rng = np.random.default_rng(97)
+    dbank, _ = _device_bank(dev, 97, {
+        "w1": (E, F, H), "w3": (E, F, H), "w2": (E, H, F),
+        "sw1": (F, H), "sw3": (F, H), "sw2": (H, F)}, 0.05)
+    wts = moe.ExpertWeights(*(a for n in ("w1", "w3", "w2") for a in dbank[n]))
+    shared = moe.SharedExpert(*(a for n in ("sw1", "sw3", "sw2") for a in dbank[n]))
+    x = _t(bf16_normal(rng, (rows, H)), dev, torch.bfloat16)
+    logits = _t(rng.normal(0, 1, (rows, E)).astype(np.float32), dev)
+    gate = _t(rng.normal(0, 1.5, rows).astype(np.float32), dev)
+    eager = moe.shared_expert_moe(x, logits, gate, wts, shared, top=top).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        moe.shared_expert_moe(x, logits, gate, wts, shared, top=top)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = moe.shared_expert_moe(x, logits, gate, wts, shared, top=top)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_np(out), _np(eager))
+        moe.shared_expert_moe(x, logits, gate, wts, shared, top=top)  # eager work between
+        torch.cuda.synchronize()
