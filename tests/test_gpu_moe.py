@@ -747,3 +747,38 @@ def test_shared_expert_moe_block_graph_replays(dev):
         np.testing.assert_array_equal(_np(out), _np(eager))
         moe.shared_expert_moe(x, logits, gate, wts, shared, top=top)  # eager work between
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_routed_moe_layer_graph_replays(dev, packed):
+    """The routed block captured in a HIP graph: every replay (with eager work
+    and synchronizations between them) equals the eager result."""
+    import torch
+    from akas_amd import moe
+
+    rows, H, F, E, top = 300, 512, 256, 16, 4
+    rng = np.random.default_rng(98)
+    bank = {}
+    for name, shape in (("w1", (E, F, H)), ("w3", (E, F, H)), ("w2", (E, H, F))):
+        bank[name] = ofp8.quantize_weight_blocks(rng.normal(0, 0.05, shape).astype(np.float32))
+    wts = moe.ExpertWeights(*(_t(a, dev) for n in ("w1", "w3", "w2") for a in bank[n]))
+    x = _t(bf16_normal(rng, (rows, H)), dev, torch.bfloat16)
+    logits = _t(rng.normal(0, 1, (rows, E)).astype(np.float32), dev)
+    kw = dict(top=top, packed=packed, max_block_m=128 if packed else 64)
+    eager = moe.routed_moe(x, logits, None, wts, **kw).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        moe.routed_moe(x, logits, None, wts, **kw)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = moe.routed_moe(x, logits, None, wts, **kw)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_np(out), _np(eager))
+        moe.routed_moe(x, logits, None, wts, **kw)  # eager work between
+        torch.cuda.synchronize()
