@@ -119,6 +119,22 @@ def test_fp8_linear_narrow_tiles_match_two_step(dev, m, n):
     assert rel_fro(y.cpu().numpy(), ofp8.fp8_linear(x, codes, scales)) < 1e-4
 
 
+@pytest.mark.parametrize("m,k,n", [(1, 8192, 2048), (8, 8192, 2048), (16, 4096, 6144)])
+def test_fp8_linear_deep_k_fused_small(dev, m, k, n):
+    """Up to 16 rows the wide kernel quantizes the whole activation slab into
+    LDS, deep K included (K=8192: a 132 KB slab), within the oracle bound."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(m + k)
+    codes, scales = block_weights(rng, (n, k))
+    x = bf16_normal(rng, (m, k), outliers=0.01)
+    y = ops.fp8_linear(_t(x, dev, torch.bfloat16), _t(codes, dev), _t(scales, dev),
+                       out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert rel_fro(y.cpu().numpy(), ofp8.fp8_linear(x, codes, scales)) < 1e-4
+
+
 @pytest.mark.parametrize("m,k,n", [(64, 8192, 2048), (17, 4096, 512), (40, 4096, 1040),
                                    (256, 4096, 6144), (100, 6144, 480), (128, 8192, 2048)])
 def test_fp8_linear_deep_k_partitions(dev, m, k, n):
