@@ -13,7 +13,9 @@ step time.  Every step reads a different copy of the weights (more than
 Also reported (``extras``): the prefill-shape GEMMs (M=8192), the MoE decode
 layer (T=256), the skewed MoE prefill layer (T=16384), the fused RMSNorm +
 quantizer (16384 x 2048) and the shared-expert (Qwen3.5 block-fp8) MoE block
-at decode (T=64, 256 experts, top 8), in TFLOP/s and GB/s; ``roofline`` for the dominant kernel (HIP-event timing of that kernel
+at decode (T=64, 256 experts, top 8), in TFLOP/s and GB/s, each block timed
+as one of four captured back to back in a graph (as a decode step graph holds
+many layers); ``roofline`` for the dominant kernel (HIP-event timing of that kernel
 alone); ``cpu_baseline`` from the oracle's C restatement on the host cores.
 
     python bench.py [--steps K] [--warmup W] [--no-extras] [--no-cpu]
@@ -213,6 +215,9 @@ def prefill_gemms(torch, dev, steps):
     return res
 
 
+LAYERS_PER_GRAPH = 4  # MoE blocks captured back to back in one graph
+
+
 def moe_layer_bench(torch, dev, tokens, zipf, steps):
     from akas_amd import moe
 
@@ -234,9 +239,11 @@ def moe_layer_bench(torch, dev, tokens, zipf, steps):
                                   max_block_m=128 if packed else 64,
                                   product_dtype=torch.bfloat16, activation_dtype=torch.bfloat16,
                                   contribution_dtype=torch.bfloat16)
-    g = graph_of(torch, fn, 1)
+    # Several layers per graph, as a decode program captures a whole step:
+    # the per-replay graph launch is shared by LAYERS_PER_GRAPH layers.
+    g = graph_of(torch, fn, LAYERS_PER_GRAPH)
     g.replay()
-    ms = time_kernel(torch, lambda i: g.replay(), steps)
+    ms = time_kernel(torch, lambda i: g.replay(), steps) / LAYERS_PER_GRAPH
     _, routing = moe.routed_moe(x, logits, None, wts, top=top, return_routing=True)
     counts = routing["counts"].cpu().numpy()
     active_experts = int((counts > 0).sum())
@@ -270,9 +277,9 @@ def shared_expert_block_bench(torch, dev, tokens=64, steps=10):
     logits = torch.from_numpy(rng.normal(0, 1, (tokens, E)).astype(np.float32)).to(dev)
     gate = torch.from_numpy(rng.normal(0, 1, tokens).astype(np.float32)).to(dev)
     fn = lambda i: moe.shared_expert_moe(x, logits, gate, wts, shared, top=top)
-    g = graph_of(torch, fn, 1)
+    g = graph_of(torch, fn, LAYERS_PER_GRAPH)
     g.replay()
-    ms = time_kernel(torch, lambda i: g.replay(), steps)
+    ms = time_kernel(torch, lambda i: g.replay(), steps) / LAYERS_PER_GRAPH
     ids = torch.topk(logits.to(torch.bfloat16).float(), top, dim=1).indices
     active_experts = int(torch.unique(ids).numel())
     wbytes = (active_experts + 1) * 3 * F * H
