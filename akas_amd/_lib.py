@@ -34,6 +34,8 @@ SIGNATURES = {
     "akas_biased_softmax_router": (_i, [_p, _p, _p, _p, _i64, _i, _i, _f, _p]),
     "akas_router": (_i, [_p, _p, _p, _i64, _i, _i, _p]),
     "akas_moe_groups": (_i, [_p, _p, _p, _i64, _i, _p]),
+    "akas_router_quantize": (_i, [_p, _p, _p, _p, _i64, _i, _i, _f, _i, _i, _p, _i, _p, _p,
+                                  _i64, _p]),
     "akas_fp8_experts_workspace_size": (_sz, [_i64, _i, _i, _i64, _i]),
     "akas_fp8_experts": (_i, [_p, _i, _p, _p, _i, _p, _p, _p, _i, _p, _sz, _i64, _i, _i,
                               _i64, _i64, _i, _p]),

@@ -6,6 +6,7 @@
 // selection compares IEEE float32 scores with lowest-index tie breaking and
 // the route compaction is an ordered block scan, never an atomic cursor.
 #include "common.h"
+#include "quant_group.h"
 
 namespace akas {
 
@@ -157,14 +158,11 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ l
 constexpr int kRowTop = 8;
 
 template <int SOFTMAX, int BF16>
-__global__ __launch_bounds__(256) void router_row16_kernel(const float* __restrict__ logits,
-                                                           const float* __restrict__ bias,
-                                                           int32_t* __restrict__ ids,
-                                                           float* __restrict__ weights,
-                                                           int64_t rows, int experts, int top,
-                                                           float scale, int normalize) {
+AKAS_DEV void router_row16(const float* __restrict__ logits, const float* __restrict__ bias,
+                           int32_t* __restrict__ ids, float* __restrict__ weights, int64_t rows,
+                           int experts, int top, float scale, int normalize, int64_t block) {
   const int lane = threadIdx.x & 63, l = lane & 15;
-  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  const int64_t row = (block * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
   const bool live = row < rows;
   const float* lg = logits + (live ? row : 0) * experts;  // spare rows read row 0, never stored
   // base: the value a chosen expert contributes (the logit, or its sigmoid);
@@ -246,6 +244,47 @@ __global__ __launch_bounds__(256) void router_row16_kernel(const float* __restri
   if (live && l < top) {
     ids[row * top + l] = mine_id;
     weights[row * top + l] = w;
+  }
+}
+
+template <int SOFTMAX, int BF16>
+__global__ __launch_bounds__(256) void router_row16_kernel(const float* __restrict__ logits,
+                                                           const float* __restrict__ bias,
+                                                           int32_t* __restrict__ ids,
+                                                           float* __restrict__ weights,
+                                                           int64_t rows, int experts, int top,
+                                                           float scale, int normalize) {
+  router_row16<SOFTMAX, BF16>(logits, bias, ids, weights, rows, experts, top, scale, normalize,
+                              blockIdx.x);
+}
+
+// The MoE block's router and its input quantizer in one launch: the first
+// router_blocks workgroups route 16 rows each (router_row16), the rest
+// quantize x row-major, 16 groups per workgroup and pass (the quantizer's
+// grid-stride loop, same quantize8, so the codes are the quantizer's).  The
+// two halves share nothing; one launch instead of two at decode sizes.
+template <int SOFTMAX, int DT>
+__global__ __launch_bounds__(256) void router_quantize_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int32_t* __restrict__ ids,
+    float* __restrict__ weights, int64_t rows, int experts, int top, float scale, int normalize,
+    int router_blocks, const void* __restrict__ x, uint8_t* __restrict__ codes,
+    float* __restrict__ scales, int64_t groups) {
+  if ((int)blockIdx.x < router_blocks) {
+    router_row16<SOFTMAX, 0>(logits, bias, ids, weights, rows, experts, top, scale, normalize,
+                             blockIdx.x);
+    return;
+  }
+  const int lane16 = threadIdx.x & 15;
+  const int64_t qblocks = (int64_t)gridDim.x - router_blocks;
+  const int64_t first = (((int64_t)blockIdx.x - router_blocks) * blockDim.x + threadIdx.x) >> 4;
+  const int64_t stride = (qblocks * blockDim.x) >> 4;
+  for (int64_t g = first; g < groups; g += stride) {
+    const int64_t base = g * kBlock + lane16 * 8;
+    float v[8], sc;
+    load8<DT>(x, base, v);
+    const uint2 c = quantize8(v, sc);
+    *reinterpret_cast<uint2*>(codes + base) = c;
+    if (lane16 == 0) scales[g] = sc;
   }
 }
 
@@ -690,6 +729,43 @@ extern "C" int akas_router(const float* logits, int32_t* ids, float* weights, in
   if (st != AKAS_OK || r == 0) return st;
   launch_router<1, 1>(logits, nullptr, ids, weights, r, experts, top, 1.0f, 1,
                       reinterpret_cast<hipStream_t>(stream));
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_router_quantize(const float* logits, const float* bias, int32_t* ids,
+                                    float* weights, int64_t r, int experts, int top, float scale,
+                                    int softmax, int normalize, const void* x, int x_dtype,
+                                    uint8_t* codes, float* scales, int64_t k, void* stream) {
+  int st = check_router(logits, ids, weights, r, experts, top);
+  if (st != AKAS_OK) return st;
+  if (experts > 64 || top > kRowTop || k <= 0 || k % kBlock) return AKAS_ERR_GEOMETRY;
+  if (x_dtype != AKAS_DTYPE_F32 && x_dtype != AKAS_DTYPE_F16 && x_dtype != AKAS_DTYPE_BF16)
+    return AKAS_ERR_DTYPE;
+  if (r == 0) return AKAS_OK;
+  if (!x || !codes || !scales) return AKAS_ERR_NULL;
+  const int64_t groups = r * (k / kBlock);
+  const int64_t rblocks = (r + 15) / 16, want = (groups + 15) / 16;
+  const int64_t qblocks = want < 8192 ? want : 8192;
+  if (rblocks + qblocks > 0x7FFFFFFF) return AKAS_ERR_GEOMETRY;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)(rblocks + qblocks));
+  auto go = [&](auto SM, auto XD) {
+    router_quantize_kernel<decltype(SM)::value, decltype(XD)::value><<<grid, 256, 0, s>>>(
+        logits, bias, ids, weights, r, experts, top, scale, normalize, (int)rblocks, x, codes,
+        scales, groups);
+  };
+  auto by_x = [&](auto SM) {
+    switch (x_dtype) {
+      case AKAS_DTYPE_F32: go(SM, DtypeTag<AKAS_DTYPE_F32>{}); break;
+      case AKAS_DTYPE_F16: go(SM, DtypeTag<AKAS_DTYPE_F16>{}); break;
+      default: go(SM, DtypeTag<AKAS_DTYPE_BF16>{});
+    }
+  };
+  if (softmax)
+    by_x(DtypeTag<1>{});
+  else
+    by_x(DtypeTag<0>{});
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }

@@ -5,8 +5,8 @@ policy rewrites that the LFM2-MoE decode/prefill programs use
 (``fused_swiglu``, ``packed``, bf16 intermediate dtypes;
 src/akas/ops/moe/definition.py:442-540, 677-793, 951-1053):
 
-    router -> quantized_routes -> quantize(x)
-      [-> expert_pack] -> fp8_expert_swiglu (or expert_partial x2 ->
+    router + quantize(x) (one launch up to 64 experts and top 8)
+      -> quantized_routes [-> expert_pack] -> fp8_expert_swiglu (or expert_partial x2 ->
       swiglu_experts -> quantize) -> expert_partial(down, routed_input)
       -> routed_combine
 
@@ -100,14 +100,15 @@ class SharedExpert:
 
 
 def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed, max_block_m,
-                          product_dtype, activation_dtype, contribution_dtype):
+                          product_dtype, activation_dtype, contribution_dtype, quantized=None):
     """Routes, FP8 activations and the grouped expert products:
-    ``[T, top, H]`` contributions in ``contribution_dtype``."""
+    ``[T, top, H]`` contributions in ``contribution_dtype``.  ``quantized``:
+    x's codes and scales when the caller made them already."""
     rows, hidden = x.shape
     experts = weights.experts
     counts, routes = ops.quantized_routes(ids, active, experts=experts)
     tile_experts = tile_rows = None  # the kernels locate tiles from counts
-    codes, scales = ops.quantize(x)
+    codes, scales = ops.quantize(x) if quantized is None else quantized
     common = dict(r=rows, top=top, max_block_m=max_block_m)
     offsets = None
     if packed:
@@ -157,7 +158,14 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
     rows = x.shape[0]
     if active is None:
         active = _all_active(rows, x.device)
-    if router == "biased_router":
+    quantized = None
+    if weights.experts <= 64 and top <= 8 and x.shape[1] % ops.BLOCK == 0:
+        # router and x's quantizer share one launch (they share no data)
+        ids, probability, codes, scales = ops.router_quantize(
+            logits, bias, x, top=top, softmax=router == "biased_softmax_router", scale=scale,
+            normalize=normalize)
+        quantized = (codes, scales)
+    elif router == "biased_router":
         ids, probability = ops.biased_router(logits, bias, top=top, scale=scale,
                                              normalize=normalize)
     else:
@@ -165,7 +173,8 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
     contributions, counts, routes = _expert_contributions(
         x, ids, active, weights, top=top, fused_swiglu=fused_swiglu, packed=packed,
         max_block_m=max_block_m, product_dtype=product_dtype,
-        activation_dtype=activation_dtype, contribution_dtype=contribution_dtype)
+        activation_dtype=activation_dtype, contribution_dtype=contribution_dtype,
+        quantized=quantized)
     out = ops.routed_combine(contributions, probability, active)
     if return_routing:
         return out, dict(ids=ids, weights=probability, counts=counts, routes=routes)

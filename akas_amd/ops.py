@@ -297,6 +297,30 @@ def router(logits, *, top, ids=None, weights=None):
     return ids, weights
 
 
+def router_quantize(logits, bias, x, *, top, softmax=True, scale=1.0, normalize=True):
+    """The MoE block's router (``biased_softmax_router`` when ``softmax``,
+    else ``biased_router``) and ``quantize(x)`` in one launch; up to 64
+    experts and top 8.  Returns ``(ids, weights, codes, scales)``, each
+    bit-identical to the separate kinds' outputs."""
+    _need(logits, "logits", torch.float32)
+    _need(x, "x", _FLOATS)
+    r, experts = logits.shape
+    if x.dim() != 2 or x.shape[0] != r:
+        raise ValueError("router_quantize expects x [r, k] with the logits' rows")
+    k = x.shape[1]
+    if bias is not None:
+        _need(bias, "bias", torch.float32, (experts,))
+    ids = torch.empty((r, top), dtype=torch.int32, device=logits.device)
+    weights = torch.empty((r, top), dtype=torch.float32, device=logits.device)
+    codes = torch.empty((r, k), dtype=torch.uint8, device=x.device)
+    scales = torch.empty((r, k // BLOCK), dtype=torch.float32, device=x.device)
+    check(_lib.load().akas_router_quantize(
+        _ptr(logits), _ptr(bias), _ptr(ids), _ptr(weights), r, experts, top, float(scale),
+        int(bool(softmax)), int(bool(normalize)), _ptr(x), _dt(x.dtype), _ptr(codes), _ptr(scales),
+        k, _stream()), "router_quantize")
+    return ids, weights, codes, scales
+
+
 def moe_groups(ids, *, experts=None, routes=None):
     """``moe_groups(r, top): ids -> experts, routes``, the block-fp8 decode
     variant's route tables (src/akas/ops/moe/cuda.py:1978-2008): per (row,

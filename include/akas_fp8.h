@@ -198,6 +198,21 @@ int akas_router(const float* logits, int32_t* ids, float* weights, int64_t r, in
                 int top, void* stream);
 
 /*
+ * The MoE block's router and its activation quantizer in one launch, for
+ * blocks whose router takes the 16-lanes-per-row form (experts <= 64,
+ * top <= 8).  No counterpart in the reference: it fuses two of its kinds,
+ * biased_router / biased_softmax_router (softmax != 0) over logits and bias
+ * (src/akas/ops/moe/kernel.py:154-203, :444-499) and quantize over x [r, k]
+ * (src/akas/quantization/activations/fp8/cuda.py:10-56), which share no
+ * data.  ids, weights, codes and scales are bit-identical to the two
+ * separate entry points' outputs.
+ */
+int akas_router_quantize(const float* logits, const float* bias, int32_t* ids, float* weights,
+                         int64_t r, int experts, int top, float scale, int softmax, int normalize,
+                         const void* x, int x_dtype, uint8_t* codes, float* scales, int64_t k,
+                         void* stream);
+
+/*
  * moe_groups(r, top): ids -> experts, routes (the block-fp8 decode variant's
  * route tables).  Replaces src/akas/ops/moe/cuda.py:1978-2008.  For each
  * (row, rank) group g of ids [r, top]: experts[g] = ids[g] when no earlier

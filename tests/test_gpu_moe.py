@@ -782,3 +782,30 @@ def test_routed_moe_layer_graph_replays(dev, packed):
         np.testing.assert_array_equal(_np(out), _np(eager))
         moe.routed_moe(x, logits, None, wts, **kw)  # eager work between
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("rows,experts,top,k,x_dtype,softmax,with_bias", [
+    (1, 64, 4, 2048, "bfloat16", True, False), (257, 64, 4, 2048, "float32", False, True),
+    (16384, 64, 4, 2048, "bfloat16", True, True), (33, 32, 6, 512, "float16", False, False),
+    (5, 7, 3, 256, "bfloat16", True, True)])
+def test_router_quantize_matches_separate_kinds(dev, rows, experts, top, k, x_dtype, softmax,
+                                                with_bias):
+    """The block's one-launch router + quantizer: ids, weights, codes and
+    scales bit-identical to the router kind and the quantize kind run apart."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(rows + experts)
+    logits = _t(rng.normal(0, 1, (rows, experts)).astype(np.float32), dev)
+    bias = _t(rng.normal(0, 0.1, experts).astype(np.float32), dev) if with_bias else None
+    x = _t(bf16_normal(rng, (rows, k), outliers=0.01), dev, getattr(torch, x_dtype))
+    ids, w, codes, scales = ops.router_quantize(logits, bias, x, top=top, softmax=softmax,
+                                                scale=1.5, normalize=True)
+    if softmax:
+        eids, ew = ops.biased_softmax_router(logits, bias, top=top, scale=1.5)
+    else:
+        eids, ew = ops.biased_router(logits, bias, top=top, scale=1.5, normalize=True)
+    ec, es = ops.quantize(x)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, eids) and torch.equal(w.view(torch.int32), ew.view(torch.int32))
+    assert torch.equal(codes, ec) and torch.equal(scales.view(torch.int32), es.view(torch.int32))
