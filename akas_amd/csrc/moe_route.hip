@@ -776,7 +776,10 @@ extern "C" int akas_quantized_routes(const int32_t* ids, const int32_t* active, 
   if (r < 0 || experts < 1 || top < 1 || r * top > 0x7FFFFFFF) return AKAS_ERR_GEOMETRY;
   if (!counts || (r > 0 && (!ids || !active || !routes))) return AKAS_ERR_NULL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (top == 4 && r % 4 == 0 && reinterpret_cast<uintptr_t>(active) % 16 == 0 &&
+  // routes4_kernel's first pass loads ids[0..15] and active[0..3]
+  // unconditionally, so it needs at least four rows; an empty batch takes
+  // the generic kernel, which only writes counts[e] = 0.
+  if (top == 4 && r >= 4 && r % 4 == 0 && reinterpret_cast<uintptr_t>(active) % 16 == 0 &&
       reinterpret_cast<uintptr_t>(ids) % 16 == 0)
     routes4_kernel<<<experts, 1024, 0, s>>>(ids, active, counts, routes, r);
   else

@@ -204,6 +204,78 @@ def test_fp8_linear_config1_and_out_dtypes(dev, out_dtype):
     assert rel_fro(got, exp) < (1e-4 if out_dtype == "float32" else 4e-3)
 
 
+# Shapes that select the DMA-fed 256x256 prefill kernel (more than 256 rows,
+# N a multiple of 128, at least 240 tiles): ragged last row tiles (M % 256 of
+# 1, 16 and 208 rows) and a half-width last column tile (N % 256 == 128).
+DMA_CASES = [(2000, 512, 7808), (1537, 384, 10112), (4097, 256, 3840), (2304, 1024, 6784)]
+
+
+@pytest.mark.parametrize("m,k,n", DMA_CASES)
+def test_projection_exact_products_dma(dev, m, k, n):
+    """The prefill kernel on exact products with distinct per-row and
+    per-block binary scales: the whole output equals the float64 oracle bit
+    for bit, so a misplaced row, column, k-block or scale index fails."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(m + 3 * n)
+    x = exact_codes(rng, (m, k))
+    w = exact_codes(rng, (n, k))
+    xs = (2.0 ** rng.integers(-6, 2, (m, k // 128))).astype(np.float32)
+    ws = (2.0 ** rng.integers(-6, 2, ((n + 127) // 128, k // 128))).astype(np.float32)
+    exp = ofp8.fp8_linear(x, w, ws, activation_scales=xs)
+    xt, xst, wt = _t(x, dev), _t(xs, dev), _t(w, dev)
+    for sdt in (torch.float32, torch.bfloat16):  # binary scales are exact in bf16
+        out = ops.projection_partial(xt, xst, wt, _t(ws, dev, sdt))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy(), exp)
+    for odt in ("bfloat16", "float16"):  # 16-bit tiles go out through LDS
+        out = ops.projection_partial(xt, xst, wt, _t(ws, dev), out_dtype=getattr(torch, odt))
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.float().cpu().numpy(), ofp8.round_to(exp, odt))
+
+
+def test_projection_dma_partitions(dev):
+    """K-partitions on the prefill kernel (2 x 128 tiles >= 240 workgroups):
+    each partition's f32 partial lands at its own offset, bit-exact."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(21)
+    m, k, n, parts = 2048, 1024, 4096, 2
+    x = exact_codes(rng, (m, k))
+    w = exact_codes(rng, (n, k))
+    xs = (2.0 ** rng.integers(-6, 2, (m, k // 128))).astype(np.float32)
+    ws = (2.0 ** rng.integers(-6, 2, (n // 128, k // 128))).astype(np.float32)
+    part = ops.projection_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev),
+                                  partitions=parts)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(part.cpu().numpy(), ofp8.projection_partial(x, xs, w, ws, parts))
+
+
+@pytest.mark.parametrize("m,k,n", [(8192, 2048, 6144), (8192, 2048, 8192), (8192, 8192, 2048)])
+def test_fp8_linear_prefill_config_shapes_full(dev, m, k, n):
+    """The three prefill GEMM shapes of the benchmark, whole output: f32 out
+    within 1e-4 relative Frobenius of the float64 oracle (bar 1e-2), and the
+    bf16 output equal to the f32 output rounded to nearest even, element for
+    element (one accumulation, two stores)."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(m + k + n)
+    codes, scales = block_weights(rng, (n, k))
+    x = bf16_normal(rng, (m, k))
+    xt, w, s = _t(x, dev, torch.bfloat16), _t(codes, dev), _t(scales, dev)
+    y32 = ops.fp8_linear(xt, w, s, out_dtype=torch.float32)
+    y16 = ops.fp8_linear(xt, w, s, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    got = y32.cpu().numpy()
+    del y32
+    np.testing.assert_array_equal(y16.float().cpu().numpy(), ofp8.bf16_round(got))
+    del y16
+    assert rel_fro(got, ofp8.fp8_linear(x, codes, scales)) < 1e-4
+
+
 @pytest.mark.parametrize("m,k,n", [(8192, 2048, 6144), (8192, 8192, 2048), (512, 2048, 8192)])
 def test_fp8_linear_prefill_shapes(dev, m, k, n):
     import torch

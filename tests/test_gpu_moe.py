@@ -146,6 +146,42 @@ def test_quantized_routes_empty_batch(dev):
     assert (_np(routes) == -1).all()
 
 
+@pytest.mark.parametrize("top", [4, 2])
+def test_quantized_routes_zero_rows(dev, top):
+    """A batch of no rows (zero-element tensors, whose device pointers are
+    null): every count is 0 and nothing else is touched
+    (``tests/test_lfm_moe.py:204-214``).  top == 4 is the four-rows-per-thread
+    kernel's shape, which must not run on an empty batch."""
+    import torch
+    from akas_amd import ops
+
+    ids = torch.empty((0, top), dtype=torch.int32, device=dev)
+    active = torch.empty((0,), dtype=torch.int32, device=dev)
+    counts = torch.full((64,), 7, dtype=torch.int32, device=dev)
+    counts, routes = ops.quantized_routes(ids, active, experts=64, counts=counts)
+    assert tuple(routes.shape) == (64, 0)
+    assert not _np(counts).any()
+
+
+def test_routed_moe_zero_rows(dev):
+    """The routed MoE block on an empty batch returns an empty f32 output."""
+    import torch
+    from akas_amd import moe
+
+    rng = np.random.default_rng(2)
+    H, F, E = 256, 128, 8
+    bank = {}
+    for name, shape in (("w1", (E, F, H)), ("w3", (E, F, H)), ("w2", (E, H, F))):
+        bank[name] = ofp8.quantize_weight_blocks(rng.normal(0, 0.05, shape).astype(np.float32))
+    wts = moe.ExpertWeights(*(_t(a, dev) for n in ("w1", "w3", "w2") for a in bank[n]))
+    x = torch.empty((0, H), dtype=torch.bfloat16, device=dev)
+    logits = torch.empty((0, E), dtype=torch.float32, device=dev)
+    for fused in (True, False):
+        out = moe.routed_moe(x, logits, None, wts, top=4, fused_swiglu=fused)
+        torch.cuda.synchronize()
+        assert tuple(out.shape) == (0, H) and out.dtype == torch.float32
+
+
 @pytest.mark.parametrize("rows,top,experts,maxm", [(33, 3, 7, 64), (257, 3, 7, 128), (1, 4, 64, 64),
                                                    (16384, 4, 64, 128)])
 def test_expert_tile_map(dev, rows, top, experts, maxm):
@@ -557,6 +593,53 @@ def test_routed_moe_layer_lfm2_dims(dev, lfm2_bank, rows, packed, zipf):
     exp, _, _ = omoe.moe_layer(x, logits, np.zeros(E, np.float32), *host, 4,
                                activation_dtype="bfloat16", contribution_dtype="bfloat16")
     assert rel_fro(_np(out), exp) < 1e-2
+
+
+def test_routed_moe_layer_zipf_prefill_full_size(dev, lfm2_bank):
+    """The skewed prefill batch of the benchmark: T = 16384 tokens, Zipf(1.1)
+    per-expert logit offsets, packed 128-aligned experts on the DMA-fed
+    256-row tiles (the top expert holds about 14.6k routed rows, 57 tiles).
+    The whole batch runs on the device; the routes are compared in full and
+    the layer output on a token sample holding, for every live expert, its
+    first two and last two routed tokens, plus every token of the largest
+    expert's last 256-row tile.  Tokens are independent in the layer
+    equation, so the oracle runs on the sample alone."""
+    import torch
+    from akas_amd import moe
+
+    wts, host = lfm2_bank
+    E, H, T, top = 64, 2048, 16384, 4
+    rng = np.random.default_rng(0)
+    x = bf16_normal(rng, (T, H))
+    logits = rng.normal(0, 1, (T, E)).astype(np.float32)
+    logits += (-1.1 * np.log1p(rng.permutation(E))).astype(np.float32)[None, :]
+    bf = torch.bfloat16
+    out, routing = moe.routed_moe(_t(x, dev, bf), _t(logits, dev), None, wts, top=top,
+                                  packed=True, max_block_m=128, product_dtype=bf,
+                                  activation_dtype=bf, contribution_dtype=bf,
+                                  return_routing=True)
+    got = _np(out)
+    ids, _ = omoe.biased_softmax_router(logits, np.zeros(E, np.float32), top)
+    np.testing.assert_array_equal(_np(routing["ids"]), ids)
+    counts, routes = omoe.quantized_routes(ids, np.ones(T, np.int32), E)
+    np.testing.assert_array_equal(_np(routing["counts"]), counts)
+    np.testing.assert_array_equal(_np(routing["routes"]), routes)
+    big = int(np.argmax(counts))
+    assert counts[big] > 50 * 256  # the skew puts many tiles on one expert
+    sample = []
+    for e in np.nonzero(counts)[0]:
+        owners = routes[e, :counts[e]] // top
+        sample += [owners[:2], owners[-2:]]
+    owners = routes[big, :counts[big]] // top
+    sample.append(owners[256 * ((counts[big] - 1) // 256):])
+    rows = np.unique(np.concatenate(sample))
+    exp, _, _ = omoe.moe_layer(x[rows], logits[rows], np.zeros(E, np.float32), *host, top,
+                               activation_dtype="bfloat16", contribution_dtype="bfloat16")
+    assert rel_fro(got[rows], exp) < 1e-2
+    # the rows outside the sample are finite and as large as the sampled ones
+    assert np.isfinite(got).all()
+    norms = np.linalg.norm(got, axis=1)
+    assert 0.5 < np.median(norms) / np.median(np.linalg.norm(exp, axis=1)) < 2.0
 
 
 # ---------------------------------------------------------------------------
