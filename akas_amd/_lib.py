@@ -28,6 +28,7 @@ SIGNATURES = {
     "akas_quantize_weight_blocks": (_i, [_p, _p, _p, _i, _i64, _i64, _i64, _p]),
     "akas_fp8_linear_workspace_size": (_sz, [_i64, _i64, _i64]),
     "akas_fp8_linear": (_i, [_p, _i, _p, _p, _i, _p, _i, _p, _sz, _i64, _i64, _i64, _p]),
+    "akas_fp8_linear_noalloc": (_i, [_p, _i, _p, _p, _i, _p, _i, _i64, _i64, _i64, _p]),
     "akas_projection_partial": (_i, [_p, _p, _p, _p, _i, _p, _i, _i64, _i64, _i64, _i, _p]),
     "akas_projection_merge": (_i, [_p, _p, _i, _i64, _i64, _i, _p]),
     "akas_biased_router": (_i, [_p, _p, _p, _p, _i64, _i, _i, _f, _i, _p]),
@@ -83,6 +84,6 @@ def check(status, what):
     if status == OK:
         return
     text = load().akas_status_string(status).decode()
-    if status in (-1, -2, -3, -5):
+    if status in (-1, -2, -3, -5, -6):
         raise ValueError(f"{what}: {text}")
     raise AkasError(f"{what}: {text}")

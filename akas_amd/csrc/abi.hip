@@ -11,9 +11,10 @@ extern "C" const char* akas_status_string(int status) {
     case AKAS_ERR_DTYPE: return "unsupported dtype";
     case AKAS_ERR_LAUNCH: return "kernel launch failed";
     case AKAS_ERR_WORKSPACE: return "workspace missing or too small";
+    case AKAS_ERR_SCRATCH: return "problem larger than the static scratch (AKAS_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown status";
   }
 }
 
 // Entry points declared in include/akas_fp8.h (kept in step by the ABI test).
-extern "C" int akas_abi_count(void) { return 26; }
+extern "C" int akas_abi_count(void) { return 27; }

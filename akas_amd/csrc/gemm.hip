@@ -1,5 +1,8 @@
 // Dense block-scaled FP8 linear for gfx950: small-M (decode) and LDS-tiled
 // (prefill) MFMA kernels, split-K partials and the partition merge.
+#include <atomic>
+#include <mutex>
+
 #include "gemm_core.h"
 #include "gemm_dma.h"
 #include "quant_group.h"
@@ -1057,10 +1060,10 @@ extern "C" size_t akas_fp8_linear_workspace_size(int64_t r, int64_t k, int64_t o
   return n;
 }
 
-extern "C" int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const void* w_scales,
-                               int scale_dtype, void* out, int out_dtype, void* workspace,
-                               size_t workspace_bytes, int64_t r, int64_t k, int64_t o,
-                               void* stream) {
+// Host checks of fp8_linear's arguments, before any workspace is looked at.
+static int check_linear(const void* x, int x_dtype, const uint8_t* w, const void* w_scales,
+                        int scale_dtype, void* out, int out_dtype, int64_t r, int64_t k,
+                        int64_t o) {
   if (r < 0 || k <= 0 || o <= 0 || k % kBlock || o % 16 || r > 0x7FFFFFFF || o > 0x7FFFFFFF ||
       k > 0x7FFFFFFF)
     return AKAS_ERR_GEOMETRY;
@@ -1069,9 +1072,18 @@ extern "C" int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, con
   if ((uint64_t)r * k >= (1ull << 32) || (uint64_t)o * k >= (1ull << 32)) return AKAS_ERR_GEOMETRY;
   if (r == 0) return AKAS_OK;
   if (!x || !w || !w_scales || !out) return AKAS_ERR_NULL;
-  if (!workspace || workspace_bytes < akas_fp8_linear_workspace_size(r, k, o))
-    return AKAS_ERR_WORKSPACE;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  return AKAS_OK;
+}
+
+// fp8_linear on validated arguments (r > 0) with a workspace of at least
+// akas_fp8_linear_workspace_size(r, k, o) bytes.  What the workspace held
+// before the call never reaches the output: the only workspace bytes read
+// that the call did not write are the padding rows of the last 16-row
+// activation tile, whose products land in output rows past r, which are
+// never stored.  So the workspace needs no clearing between calls.
+static int run_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const void* w_scales,
+                          int scale_dtype, void* out, int out_dtype, void* workspace, int64_t r,
+                          int64_t k, int64_t o, hipStream_t s) {
   if (r <= kFusedQuantizeRows) {
     DenseArgs f{nullptr, nullptr, w, w_scales, out, o, 0, (int)r, (int)o, (int)k,
                 (int)(k / kBlock), scale_dtype, out_dtype, x, x_dtype};
@@ -1105,6 +1117,67 @@ extern "C" int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, con
   const int st = launch_quantize(x, x_dtype, codes, scales, r, k, frag, s);
   if (st != AKAS_OK) return st;
   return frag ? launch_split_frag(a, s) : launch_dense(a, 1, s);
+}
+
+extern "C" int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const void* w_scales,
+                               int scale_dtype, void* out, int out_dtype, void* workspace,
+                               size_t workspace_bytes, int64_t r, int64_t k, int64_t o,
+                               void* stream) {
+  const int st = check_linear(x, x_dtype, w, w_scales, scale_dtype, out, out_dtype, r, k, o);
+  if (st != AKAS_OK || r == 0) return st;
+  if (!workspace || workspace_bytes < akas_fp8_linear_workspace_size(r, k, o))
+    return AKAS_ERR_WORKSPACE;
+  return run_fp8_linear(x, x_dtype, w, w_scales, scale_dtype, out, out_dtype, workspace, r, k, o,
+                        reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// fp8_linear without allocation: the workspace is `scratch`, a file-scope
+// device array of AKAS_NOALLOC_SCRATCH_BYTES.  Every GPU the library runs on
+// holds its own copy until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it names a stand-in, not device
+// memory): the device address comes from hipGetSymbolAddress, taken once per
+// device with that device current, and cached per device.  All calls on one
+// GPU share its array, so calls that overlap in time on one GPU (different
+// streams, or different host threads) race on it; calls ordered on one
+// stream do not.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[AKAS_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> scratch_address[kMaxDevices];
+static std::mutex scratch_mutex;
+
+// Device address of the current device's `scratch`, or null when the device
+// index is out of range or the runtime cannot resolve the symbol.
+static void* current_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  void* p = scratch_address[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  p = scratch_address[dev].load(std::memory_order_relaxed);
+  if (!p) {
+    void* q = nullptr;
+    if (hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) != hipSuccess || !q) return nullptr;
+    scratch_address[dev].store(q, std::memory_order_release);
+    p = q;
+  }
+  return p;
+}
+
+extern "C" int akas_fp8_linear_noalloc(const void* x, int x_dtype, const uint8_t* w,
+                                       const void* w_scales, int scale_dtype, void* out,
+                                       int out_dtype, int64_t r, int64_t k, int64_t o,
+                                       void* stream) {
+  const int st = check_linear(x, x_dtype, w, w_scales, scale_dtype, out, out_dtype, r, k, o);
+  if (st != AKAS_OK || r == 0) return st;
+  if (akas_fp8_linear_workspace_size(r, k, o) > AKAS_NOALLOC_SCRATCH_BYTES)
+    return AKAS_ERR_SCRATCH;
+  void* ws = current_scratch();
+  if (!ws) return AKAS_ERR_LAUNCH;
+  return run_fp8_linear(x, x_dtype, w, w_scales, scale_dtype, out, out_dtype, ws, r, k, o,
+                        reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int akas_projection_partial(const uint8_t* x, const float* activation_scales,

@@ -54,6 +54,10 @@ extern "C" {
 #define AKAS_ERR_DTYPE -3    /* unsupported dtype code */
 #define AKAS_ERR_LAUNCH -4   /* HIP launch failed */
 #define AKAS_ERR_WORKSPACE -5 /* workspace missing or too small */
+#define AKAS_ERR_SCRATCH -6   /* problem larger than the library's static scratch */
+
+/* Bytes of the static device scratch of akas_fp8_linear_noalloc (per GPU). */
+#define AKAS_NOALLOC_SCRATCH_BYTES (64u << 20)
 
 /* Library version (major*10000 + minor*100 + patch). */
 int akas_version(void);
@@ -131,12 +135,31 @@ size_t akas_fp8_linear_workspace_size(int64_t r, int64_t k, int64_t o);
  * registered at src/akas/ops/linear/definition.py:1890-1914.
  * x f32/f16/bf16 [r, k]; w u8 [o, k]; w_scales f32|bf16 [ceil(o/128), k/128];
  * out f32/f16/bf16 [r, o] = quantize(x) . dequant(w)^T, f32 accumulation.
- * k % 128 == 0 and o % 16 == 0.  The workspace must be zero-filled before
- * its first use; every call leaves it zero-filled again.
+ * k % 128 == 0 and o % 16 == 0.  The workspace (at least
+ * akas_fp8_linear_workspace_size(r, k, o) bytes) needs no initialization:
+ * its prior contents never reach the output.  Calls that share a workspace
+ * must be ordered on one stream.
  */
 int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, const void* w_scales,
                     int scale_dtype, void* out, int out_dtype, void* workspace,
                     size_t workspace_bytes, int64_t r, int64_t k, int64_t o, void* stream);
+
+/*
+ * fp8_linear without allocation and without a workspace argument.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * akas_fp8_linear (bit for bit); the workspace is a static device array of
+ * AKAS_NOALLOC_SCRATCH_BYTES held by every GPU the library runs on until the
+ * process ends.  Returns AKAS_ERR_SCRATCH when
+ * akas_fp8_linear_workspace_size(r, k, o) exceeds it.  The call never calls
+ * hipMalloc or hipFree.  All calls on one GPU share its array: calls that
+ * overlap in time on one GPU (two streams, or two host threads) race;
+ * calls ordered on one stream do not.
+ */
+int akas_fp8_linear_noalloc(const void* x, int x_dtype, const uint8_t* w, const void* w_scales,
+                            int scale_dtype, void* out, int out_dtype, int64_t r, int64_t k,
+                            int64_t o, void* stream);
 
 /*
  * projection_partial(r, k, o, partitions): prequantized x, w, scales,

@@ -53,6 +53,11 @@ def test_host_validation_rejects_before_launch():
     # linear: o not a multiple of 16, workspace too small
     assert lib.akas_fp8_linear(1, 2, 1, 1, 0, 1, 0, 1, 1 << 30, 4, 256, 100, None) == -1
     assert lib.akas_fp8_linear(1, 2, 1, 1, 0, 1, 0, 1, 16, 4, 256, 128, None) == -5
+    # no-allocation linear: a workspace beyond the static scratch is refused
+    # on the host (-6), before the device is touched; no rows is a no-op
+    assert lib.akas_fp8_linear_noalloc(1, 2, 1, 1, 0, 1, 0, 16384, 4096, 2048, None) == -6
+    assert lib.akas_fp8_linear_noalloc(1, 2, 1, 1, 0, 1, 0, 4, 256, 100, None) == -1
+    assert lib.akas_fp8_linear_noalloc(None, 2, None, None, 0, None, 0, 0, 256, 128, None) == 0
     # partitions must divide k/128
     assert lib.akas_projection_partial(1, 1, 1, 1, 0, 1, 0, 4, 384, 128, 2, None) == -1
     # tile map: unsupported maximum row tile
