@@ -224,6 +224,105 @@ AKAS_DEV float load_scale_t(const void* p, int64_t i) {
 }
 
 // ---------------------------------------------------------------------------
+// Correctly rounded float32 exp, and the router's sigmoid built on it
+// ---------------------------------------------------------------------------
+//
+// exp_rn(x) = RN32(e^x), the float32 nearest to the exact exponential, for
+// every float32 x whose result is a normal float32 or overflows (x >=
+// -87.33); below that the result is within one subnormal step.
+//
+// Fast path: e^x in double (the device library's exp, within 1 ulp of
+// double), rounded once to float32.  That rounding can only go wrong when
+// e^x lies within about 1 double ulp of a float32 rounding midpoint, so any
+// result whose low 29 fraction bits (the bits below float32 precision) lie
+// within 16 units of the midpoint pattern 2^28 takes the slow path: e^x in
+// double-double arithmetic (about 100 bits), rounded to float32 from both
+// words.  An exhaustive scan of all float32 inputs finds about fifty such
+// inputs in the range a sigmoid needs; the closest lies 1.27 double ulps
+// from a midpoint.
+namespace dd {
+// Double-double arithmetic: value = hi + lo, |lo| <= ulp(hi) / 2.  The
+// error-free transformations need every operation rounded on its own, so
+// each function turns contraction off for its body.
+struct Dd {
+  double hi, lo;
+};
+AKAS_DEV Dd quick_two_sum(double a, double b) {
+#pragma clang fp contract(off)
+  const double s = a + b;
+  return {s, b - (s - a)};
+}
+AKAS_DEV Dd two_sum(double a, double b) {
+#pragma clang fp contract(off)
+  const double s = a + b, bb = s - a;
+  return {s, (a - (s - bb)) + (b - bb)};
+}
+AKAS_DEV Dd add(const Dd& a, const Dd& b) {
+#pragma clang fp contract(off)
+  const Dd s = two_sum(a.hi, b.hi), t = two_sum(a.lo, b.lo);
+  const Dd u = quick_two_sum(s.hi, s.lo + t.hi);
+  return quick_two_sum(u.hi, u.lo + t.lo);
+}
+AKAS_DEV Dd mul(const Dd& a, const Dd& b) {
+#pragma clang fp contract(off)
+  const double p = a.hi * b.hi;
+  const double e = __builtin_fma(a.hi, b.hi, -p);
+  return quick_two_sum(p, e + (a.hi * b.lo + a.lo * b.hi));
+}
+// a / n for a small positive integer n: the remainder of the leading
+// quotient is exact through one FMA.
+AKAS_DEV Dd div_int(const Dd& a, double n) {
+#pragma clang fp contract(off)
+  const double q = a.hi / n;
+  const double rem = __builtin_fma(-q, n, a.hi);
+  return quick_two_sum(q, (rem + a.lo) / n);
+}
+// e^x for |x| <= 104: x = k ln2 + r with |r| <= ln2/2, ln2 split as
+// kLn2Hi (trailing zero bits, so k * kLn2Hi is exact and x - k * kLn2Hi is
+// exact by Sterbenz's lemma) + kLn2Lo; e^r by its Taylor series to degree
+// 20 in nested form 1 + r(1 + r/2(1 + r/3(...))) (truncation below 2^-90
+// relative); then the exact scaling by 2^k.
+AKAS_DEV Dd exp_dd(double x) {
+#pragma clang fp contract(off)
+  constexpr double kLn2Hi = 6.93147180369123816490e-01;  // 0x3FE62E42FEE00000
+  constexpr double kLn2Lo = 1.90821492927058770002e-10;  // ln2 - kLn2Hi
+  constexpr double kInvLn2 = 1.44269504088896338700e+00;
+  const double k = __builtin_rint(x * kInvLn2);
+  const double rhi = __builtin_fma(-k, kLn2Hi, x);  // exact
+  const double p = k * kLn2Lo;
+  const Dd r = add(Dd{rhi, 0.0}, Dd{-p, -__builtin_fma(k, kLn2Lo, -p)});
+  Dd t{1.0, 0.0};
+  for (int i = 20; i >= 1; --i) t = add(Dd{1.0, 0.0}, div_int(mul(r, t), (double)i));
+  return {__builtin_ldexp(t.hi, (int)k), __builtin_ldexp(t.lo, (int)k)};
+}
+}  // namespace dd
+
+// Distance, in units of the last double bit, of a positive double from the
+// float32 rounding midpoint of its binade (normal float32 range).
+AKAS_DEV int64_t midpoint_distance(double v) {
+  const int64_t low = (int64_t)(__double_as_longlong(v) & ((1ll << 29) - 1));
+  const int64_t d = low - (1ll << 28);
+  return d < 0 ? -d : d;
+}
+
+AKAS_DEV float exp_rn(float x) {
+  const double e = exp((double)x);
+  if (midpoint_distance(e) > 16) return (float)e;
+  const dd::Dd y = dd::exp_dd((double)x);
+  // hi is the double nearest to hi + lo; only when hi is itself a float32
+  // midpoint does lo decide the direction (lo == 0: ties to even).
+  if (midpoint_distance(y.hi) != 0 || y.lo == 0.0) return (float)y.hi;
+  const long long b = __double_as_longlong(y.hi);
+  return (float)__longlong_as_double(y.lo > 0.0 ? b + 1 : b - 1);
+}
+
+// The sigmoid router's score term 1 / (1 + e^-l) in float32 with a
+// correctly rounded exponential and IEEE addition and division: the
+// reference kernel's float32 expression (src/akas/ops/moe/kernel.py:171,
+// :189-190) with every step rounded once.
+AKAS_DEV float router_sigmoid(float l) { return __fdiv_rn(1.0f, 1.0f + exp_rn(-l)); }
+
+// ---------------------------------------------------------------------------
 // SwiGLU element: g / (1 + exp(-g)) * u in float32
 // (src/akas/ops/activation/kernel.py:83-88).  One definition shared by the
 // fused and the separate kernels so their results are bit-identical.

@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ l
     const int e = s * 64 + lane;
     float v = 0.f, sc = -__builtin_inff();
     if (s < slots && e < experts) {
-      v = SOFTMAX ? (BF16 ? round_bf16(l[e]) : l[e]) : __fdiv_rn(1.0f, 1.0f + expf(-l[e]));
+      v = SOFTMAX ? (BF16 ? round_bf16(l[e]) : l[e]) : router_sigmoid(l[e]);
       sc = v + (bias ? bias[e] : 0.f);
     }
     base[s] = v;
@@ -173,7 +173,7 @@ AKAS_DEV void router_row16(const float* __restrict__ logits, const float* __rest
     const int e = l * 4 + i;
     float v = 0.f, sc = -__builtin_inff();
     if (e < experts) {
-      v = SOFTMAX ? (BF16 ? round_bf16(lg[e]) : lg[e]) : __fdiv_rn(1.0f, 1.0f + expf(-lg[e]));
+      v = SOFTMAX ? (BF16 ? round_bf16(lg[e]) : lg[e]) : router_sigmoid(lg[e]);
       sc = v + (bias ? bias[e] : 0.f);
     }
     base[i] = v;

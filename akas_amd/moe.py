@@ -62,7 +62,6 @@ def _all_active(rows, device):
 
 
 _SIDE = {}
-_SIDE_WORKSPACES = {}
 
 
 def _side_stream(device):
@@ -72,18 +71,6 @@ def _side_stream(device):
     if key not in _SIDE:
         _SIDE[key] = torch.cuda.Stream(device=device)
     return _SIDE[key]
-
-
-def _side_workspace(shapes, device):
-    """fp8_linear workspace for the side stream (the per-device one in ops
-    serves the caller's stream, which may run at the same time)."""
-    need = max(int(ops._lib.load().akas_fp8_linear_workspace_size(r, k, o)) for r, k, o in shapes)
-    key = str(device)
-    ws = _SIDE_WORKSPACES.get(key)
-    if ws is None or ws.numel() < need:
-        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
-        _SIDE_WORKSPACES[key] = ws
-    return ws
 
 
 @dataclass
@@ -227,15 +214,13 @@ def shared_expert_moe(x, logits, shared_gate, weights: ExpertWeights, shared: Sh
     # the routed experts stream their weights, and the combine waits for it.
     main = torch.cuda.current_stream(x.device)
     side = _side_stream(x.device)
-    width, hidden = shared.w1.shape[0], x.shape[1]
-    ws = _side_workspace(((rows, hidden, width), (rows, width, hidden)), x.device)
+    width = shared.w1.shape[0]
     side.wait_stream(main)
-    with torch.cuda.stream(side):
-        g = ops.fp8_linear(x, shared.w1, shared.s1, workspace=ws)
-        u = ops.fp8_linear(x, shared.w3, shared.s3, workspace=ws)
+    with torch.cuda.stream(side):  # fp8_linear takes the side stream's own workspace
+        g = ops.fp8_linear(x, shared.w1, shared.s1)
+        u = ops.fp8_linear(x, shared.w3, shared.s3)
         activated = ops.swiglu_experts(g.view(rows, 1, width), u.view(rows, 1, width))
-        shared_out = ops.fp8_linear(activated.view(rows, width), shared.w2, shared.s2,
-                                    workspace=ws)
+        shared_out = ops.fp8_linear(activated.view(rows, width), shared.w2, shared.s2)
     ids, probability = ops.router(logits, top=top)
     if routed_kinds == "groups":
         contributions = _group_contributions(x, ids, weights, top=top)

@@ -166,17 +166,29 @@ def quantize_weight_blocks(w, *, scale_dtype=torch.float32):
 # dense linear
 # ---------------------------------------------------------------------------
 
-_WORKSPACES = {}
+_WORKSPACES = {}  # (device index, stream handle) -> workspace of that stream
+_RETIRED = []     # workspaces outgrown by their stream, kept alive for good
 
 
-def linear_workspace(r, k, o, device):
-    """Cached, zero-filled workspace for :func:`fp8_linear` (per device)."""
+def linear_workspace(r, k, o, device, stream=None):
+    """Cached workspace for :func:`fp8_linear`, one per device and stream.
+
+    Calls sharing a workspace must be ordered on one stream, so each stream
+    gets its own.  When a larger problem outgrows a stream's workspace, the
+    old one is retired but never freed: a HIP graph captured earlier may
+    still hold its address.  The contents need no initialization.
+    """
     need = _lib.load().akas_fp8_linear_workspace_size(r, k, o)
-    key = torch.device(device).index if torch.device(device).index is not None else \
-        torch.cuda.current_device()
+    device = torch.device(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if stream is None:
+        stream = torch.cuda.current_stream(index)
+    key = (index, stream.cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < need:
-        ws = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
+        if ws is not None:
+            _RETIRED.append(ws)
+        ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", index))
         _WORKSPACES[key] = ws
     return ws
 
@@ -200,10 +212,32 @@ def fp8_linear(x, w, scales, *, out=None, out_dtype=None, workspace=None):
     _need(scales, "scales", _SCALES, ((o + BLOCK - 1) // BLOCK, k // BLOCK))
     out = _out(out, "out", (r, o), _out_dtype(out, out_dtype), x)
     if workspace is None:
-        workspace = linear_workspace(r, k, o, x.device)
+        workspace = linear_workspace(r, k, o, x.device)  # this stream's own
     check(_lib.load().akas_fp8_linear(
         _ptr(x), _dt(x.dtype), _ptr(w), _ptr(scales), _dt(scales.dtype), _ptr(out),
         _dt(out.dtype), _ptr(workspace), workspace.numel(), r, k, o, _stream()), "fp8_linear")
+    return out
+
+
+def fp8_linear_noalloc(x, w, scales, *, out=None, out_dtype=None):
+    """:func:`fp8_linear` on the library's static device scratch
+    (``akas_fp8_linear_noalloc``): no workspace argument and no device
+    allocation inside the call when ``out`` is given.  Problems whose
+    workspace exceeds the scratch raise ``ValueError``; calls overlapping in
+    time on one GPU race on the shared scratch."""
+    _need(x, "x", _FLOATS)
+    _need(w, "w", torch.uint8)
+    if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
+        raise ValueError("fp8_linear expects x [r, k] and w [o, k]")
+    r, k = x.shape
+    o = w.shape[0]
+    if k % BLOCK or o % 16:
+        raise ValueError("invalid FP8 projection geometry")
+    _need(scales, "scales", _SCALES, ((o + BLOCK - 1) // BLOCK, k // BLOCK))
+    out = _out(out, "out", (r, o), _out_dtype(out, out_dtype), x)
+    check(_lib.load().akas_fp8_linear_noalloc(
+        _ptr(x), _dt(x.dtype), _ptr(w), _ptr(scales), _dt(scales.dtype), _ptr(out),
+        _dt(out.dtype), r, k, o, _stream()), "fp8_linear_noalloc")
     return out
 
 

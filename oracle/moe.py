@@ -33,16 +33,72 @@ def _iterative_topk(scores, top):
     return ids
 
 
+_MIDPOINT_MARGIN = 64  # double ulps around a float32 rounding midpoint
+
+
+def _exp_rn32_exact(v):
+    """RN32(e^v) from the exact exponential (mpmath, 200 bits): the nearer of
+    the float32 neighbours of e^v, ties to the even one; +inf from the
+    overflow threshold 2^128 - 2^103 up (IEEE round-to-nearest)."""
+    import mpmath
+
+    with mpmath.workprec(200):
+        t = mpmath.exp(mpmath.mpf(float(v)))
+        if t >= mpmath.mpf(2) ** 128 - mpmath.mpf(2) ** 103:
+            return np.float32(np.inf)
+        c = np.float32(float(t))
+        if not np.isfinite(c):
+            c = np.float32(np.finfo(np.float32).max)
+        cands = (np.nextafter(c, np.float32(0)), c, np.nextafter(c, np.float32(np.inf)))
+        cands = [f for f in cands if np.isfinite(f)]
+        return min(cands, key=lambda f: (abs(mpmath.mpf(float(f)) - t),
+                                         int(np.array(f, np.float32).view(np.uint32)) & 1))
+
+
+def exp_rn32(x):
+    """Correctly rounded float32 exponential: the float32 nearest to e^x
+    (ties to even) for float32 ``x`` whose result is a normal float32 or
+    overflows.
+
+    e^x in float64 rounded once to float32 is that value unless e^x lies
+    within a few double ulps of a float32 rounding midpoint (the pattern
+    2^28 in the 29 fraction bits below float32 precision).  Results within
+    64 double ulps of one (a few dozen of all float32 inputs) are recomputed
+    from the exact exponential.  This is the exponential of the reference
+    router's float32 expression ``1 / (1 + T.exp(-l))``
+    (``src/akas/ops/moe/kernel.py:171``) rounded once, which the device's
+    sigmoid router computes as well.
+    """
+    x = np.asarray(x, np.float32)
+    flat = x.ravel()
+    with np.errstate(over="ignore"):
+        y = np.exp(flat.astype(np.float64))
+        out = y.astype(np.float32)
+    low = (y.view(np.uint64) & np.uint64((1 << 29) - 1)).astype(np.int64)
+    near = (np.abs(low - (1 << 28)) <= _MIDPOINT_MARGIN) & np.isfinite(y) & (y >= 2.0 ** -126)
+    for i in np.flatnonzero(near):
+        out[i] = _exp_rn32_exact(flat[i])
+    return out.reshape(x.shape)
+
+
+def router_sigmoid(logits):
+    """``1 / (1 + exp(-l))`` in float32: correctly rounded exponential, IEEE
+    float32 addition and division (``src/akas/ops/moe/kernel.py:171``)."""
+    logits = np.asarray(logits, np.float32)
+    return (np.float32(1) / (np.float32(1) + exp_rn32(-logits))).astype(np.float32)
+
+
 def biased_router(logits, bias, top, scale=1.0, normalize=True):
     """Sigmoid scores plus bias select; unbiased sigmoid weights combine.
 
     ``score = 1/(1+exp(-l)) + b``; weights ``sigmoid(l_sel) * scale / (sum + 1e-6)``
     (``normalize``) or ``sigmoid(l_sel) * scale``.  Follows
     ``src/akas/ops/moe/kernel.py:154-203`` and ``validation.py:138-150``.
-    Selection uses float32 sigmoid (as the device computes it).
+    Selection is on the float32 score, every operation rounded once
+    (:func:`router_sigmoid`, then an IEEE float32 addition of the bias).
     """
     logits = np.asarray(logits, np.float32)
-    sig = (np.float32(1) / (np.float32(1) + np.exp(-logits))).astype(np.float32)
+    sig = router_sigmoid(logits)
     scores = (sig + np.asarray(bias, np.float32)[None, :]).astype(np.float32)
     ids = _iterative_topk(scores, top)
     chosen = np.take_along_axis(sig.astype(np.float64), ids, axis=1)

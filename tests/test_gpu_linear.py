@@ -363,3 +363,32 @@ def test_linear_rejects_bad_geometry(dev):
     s = torch.zeros((1, 1), dtype=torch.float32, device=dev)
     with pytest.raises(ValueError):
         ops.fp8_linear(x, w, s)
+
+
+def test_fp8_linear_default_workspace_per_stream(dev):
+    """fp8_linear without an explicit workspace on two streams at once: each
+    stream has its own cached workspace, so concurrent calls do not share
+    codes and scales, and every result equals the one-stream result."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(17)
+    codes, scales = block_weights(rng, (6144, 2048))
+    w, s = _t(codes, dev), _t(scales, dev)
+    xs = [_t(bf16_normal(rng, (m, 2048), outliers=0.01), dev, torch.bfloat16)
+          for m in (64, 200, 64, 256)]
+    ref = [ops.fp8_linear(x, w, s, out_dtype=torch.float32) for x in xs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    assert (ops.linear_workspace(64, 2048, 6144, dev, streams[0]).data_ptr() !=
+            ops.linear_workspace(64, 2048, 6144, dev, streams[1]).data_ptr())
+    outs = [[None] * len(xs) for _ in streams]
+    for rep in range(20):
+        for j, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                for i, x in enumerate(xs):
+                    outs[j][i] = ops.fp8_linear(x, w, s, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    for j in range(len(streams)):
+        for i in range(len(xs)):
+            np.testing.assert_array_equal(outs[j][i].cpu().numpy(), ref[i].cpu().numpy())

@@ -101,6 +101,92 @@ def test_sigmoid_router(dev, normalize):
     np.testing.assert_allclose(_np(w), ew, rtol=2e-6, atol=1e-7)
 
 
+def test_sigmoid_router_score_every_float32(dev):
+    """The device's 1 / (1 + e^-l) equals the oracle's for every float32
+    logit on which it depends on the exponential's last bit: all l in
+    [-88.75, 17] with |l| >= 2^-26 (about 524 million values), plus the
+    tails and a sample of tinier ones.  Read through the router itself: one
+    expert, top 1, unnormalized, scale 1 makes the weight the score term."""
+    import torch
+    from akas_amd import ops
+
+    def check(bits):
+        logits = torch.from_numpy(bits.view(np.float32).reshape(-1, 1)).to(dev)
+        _, w = ops.biased_router(logits, None, top=1, normalize=False)
+        got = w.cpu().numpy().ravel()
+        exp = omoe.router_sigmoid(bits.view(np.float32))
+        bad = np.flatnonzero(got.view(np.uint32) != exp.view(np.uint32))
+        assert bad.size == 0, (bits[bad[:8]], got[bad[:8]], exp[bad[:8]])
+
+    step = 1 << 25
+    for sign, hi in ((0x80000000, 0x42B18000), (0, 0x41880000)):  # l < 0, then l > 0
+        for a in range(0x32800000, hi + 1, step):
+            check(np.arange(a, min(a + step, hi + 1), dtype=np.uint32) | np.uint32(sign))
+    rng = np.random.default_rng(9)
+    tails = np.concatenate([rng.integers(0, 0x32800000, 1 << 20),        # |l| < 2^-26
+                            rng.integers(0x42B18000, 0x7F800000, 1 << 20),  # l < -88.75
+                            rng.integers(0x41880000, 0x7F800000, 1 << 20)]).astype(np.uint32)
+    signs = np.array([0, 0x80000000, 0], np.uint32).repeat(1 << 20)
+    signs[: 1 << 20] = rng.integers(0, 2, 1 << 20).astype(np.uint32) << 31
+    check(tails | signs)
+
+
+def _logit_for_score(target, lo=0.0, hi=16.0):
+    """Smallest float32 l in [lo, hi] with router_sigmoid(l) >= target (the
+    score term is monotone in l), by bisection on the float32 patterns."""
+    a = np.full(target.shape, np.float32(lo)).view(np.uint32).astype(np.int64)
+    b = np.full(target.shape, np.float32(hi)).view(np.uint32).astype(np.int64)
+    while np.any(a < b):
+        m = (a + b) // 2
+        ok = omoe.router_sigmoid(m.astype(np.uint32).view(np.float32)) >= target
+        b = np.where(ok, m, b)
+        a = np.where(ok, a, m + 1)
+    return a.astype(np.uint32).view(np.float32)
+
+
+def test_sigmoid_router_near_ties(dev):
+    """Scores that tie exactly or differ in the last bit: logits one float32
+    step apart (whose score terms often round to the same value), and pairs
+    whose biases differ by 0.25 with the logit of the biased expert chosen
+    so that sigmoid + bias lands exactly on the other expert's score.  Ties
+    go to the lower expert index, so one wrong bit anywhere in the score
+    changes the ids."""
+    from akas_amd import ops
+
+    rng = np.random.default_rng(31)
+    rows, experts, top = 4096, 64, 4
+    bias = np.zeros(experts, np.float32)
+    bias[32:] = 0.25
+    logits = (rng.normal(0, 1, (rows, experts)) - 4).astype(np.float32)  # low background
+    r = np.arange(rows)
+    # pair A: two unbiased experts, logits one float32 step apart, either order
+    i, j = rng.integers(0, 16, rows), rng.integers(16, 32, rows)
+    u = rng.uniform(1.0, 3.0, rows).astype(np.float32)
+    up = np.nextafter(u, np.float32(np.inf))
+    swap = rng.random(rows) < 0.5
+    logits[r, i] = np.where(swap, up, u)
+    logits[r, j] = np.where(swap, u, up)
+    # pair B: an unbiased expert with score s and a biased one whose
+    # sigmoid + 0.25 rounds to s; the biased expert sits at the higher index
+    lo_e, hi_e = rng.integers(0, 16, rows), rng.integers(32, 64, rows)
+    lo_e = np.where(lo_e == i, (lo_e + 1) % 16, lo_e)
+    lb = rng.uniform(2.0, 3.0, rows).astype(np.float32)
+    s = omoe.router_sigmoid(lb)
+    lh = _logit_for_score(s - np.float32(0.25))
+    hit = (omoe.router_sigmoid(lh) + np.float32(0.25)).astype(np.float32) == s
+    assert hit.mean() > 0.9
+    logits[r, lo_e] = lb
+    logits[r, hi_e] = lh
+    ids, w = ops.biased_router(_t(logits, dev), _t(bias, dev), top=top, scale=1.0, normalize=True)
+    eids, ew = omoe.biased_router(logits, bias, top, 1.0, True)
+    np.testing.assert_array_equal(_np(ids), eids)
+    np.testing.assert_allclose(_np(w), ew, rtol=2e-6, atol=1e-7)
+    # the ties are real: equal scores among the chosen experts in most rows
+    score = (omoe.router_sigmoid(logits) + bias).astype(np.float32)
+    top_scores = np.take_along_axis(score, eids, axis=1)
+    assert (np.diff(top_scores, axis=1) == 0).any(axis=1).mean() > 0.5
+
+
 # ---------------------------------------------------------------------------
 # routes / tile map / pack
 # ---------------------------------------------------------------------------

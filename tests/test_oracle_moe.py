@@ -99,6 +99,112 @@ def test_sigmoid_router(normalize):
 
 
 # ---------------------------------------------------------------------------
+# the sigmoid router's float32 exponential
+# ---------------------------------------------------------------------------
+
+F32_MAX_MIDPOINT = 2.0 ** 128 - 2.0 ** 103  # IEEE round-to-nearest overflows from here
+
+
+def _rn32_exp_decimal(x):
+    """RN32(e^x) of one float32 ``x`` from Python's ``decimal`` exponential
+    (correctly rounded at 60 significant digits): the nearer float32
+    neighbour of the 60-digit value, ties to the even pattern.  Independent
+    of numpy's and mpmath's exponentials."""
+    from decimal import Decimal, localcontext
+
+    with localcontext() as ctx:
+        ctx.prec = 60
+        t = Decimal(float(x)).exp()
+        if t >= Decimal(F32_MAX_MIDPOINT):
+            return np.float32(np.inf)
+        c = np.float32(min(float(t), float(np.finfo(np.float32).max)))
+        best = None
+        for f in (np.nextafter(c, np.float32(0)), c, np.nextafter(c, np.float32(np.inf))):
+            if not np.isfinite(f):
+                continue
+            key = (abs(Decimal(float(f)) - t), int(np.array(f, np.float32).view(np.uint32)) & 1)
+            if best is None or key < best[0]:
+                best = (key, f)
+        return best[1]
+
+
+def _midpoint_hazards(margin=64):
+    """Every float32 x with 2^-26 <= |x|, x in [-17, 88.75] (the inputs on
+    which 1 / (1 + e^-l) depends on the exponential's last bit) whose float64
+    e^x lies within ``margin`` double ulps of a float32 rounding midpoint."""
+    found = []
+    for sign, hi in ((0, 0x42B18000), (0x80000000, 0x41880000)):
+        for a in range(0x32800000, hi + 1, 1 << 24):
+            bits = np.arange(a, min(a + (1 << 24), hi + 1), dtype=np.uint32) | np.uint32(sign)
+            y = np.exp(bits.view(np.float32).astype(np.float64))
+            low = (y.view(np.uint64) & np.uint64((1 << 29) - 1)).astype(np.int64)
+            found.append(bits[np.abs(low - (1 << 28)) <= margin])
+    return np.concatenate(found).view(np.float32)
+
+
+def test_exp_rn32_is_correctly_rounded():
+    """Where float64 e^x sits near a float32 midpoint (all of them, found by
+    an exhaustive scan of the sigmoid's input range), the oracle's exp_rn32
+    equals the decimal-derived correctly rounded value; elsewhere numpy's
+    float64 exp, within an ulp of double on a random sample and at the range
+    ends, is 64 double ulps clear of every midpoint, so its float32 rounding
+    is correct."""
+    from decimal import Decimal, localcontext
+
+    hazards = _midpoint_hazards()
+    assert 0 < hazards.size < 500
+    got = omoe.exp_rn32(hazards)
+    exp = np.array([_rn32_exp_decimal(v) for v in hazards], np.float32)
+    np.testing.assert_array_equal(got.view(np.uint32), exp.view(np.uint32))
+    # numpy's float64 exp is within 1 ulp of double on a sample of the range
+    rng = np.random.default_rng(3)
+    sample = np.concatenate([rng.uniform(-17, 88.75, 3000), rng.uniform(-1e-3, 1e-3, 1000),
+                             [88.72283, 88.72284, -17.0, 88.75]]).astype(np.float32)
+    y = np.exp(sample.astype(np.float64))
+    with localcontext() as ctx:
+        ctx.prec = 60
+        for v, yv in zip(sample, y):
+            t = Decimal(float(v)).exp()
+            assert abs(Decimal(float(yv)) - t) <= Decimal(float(np.spacing(yv)))
+    np.testing.assert_array_equal(omoe.exp_rn32(sample).view(np.uint32),
+                                  np.array([_rn32_exp_decimal(v) for v in sample],
+                                           np.float32).view(np.uint32))
+
+
+def test_exp_rn32_overflow_threshold():
+    """The largest float32 x with a finite RN32(e^x), and the next one up."""
+    x = np.float32(88.72283)
+    while np.isfinite(_rn32_exp_decimal(np.nextafter(x, np.float32(np.inf)))):
+        x = np.nextafter(x, np.float32(np.inf))
+    while not np.isfinite(_rn32_exp_decimal(x)):
+        x = np.nextafter(x, np.float32(0))
+    up = np.nextafter(x, np.float32(np.inf))
+    got = omoe.exp_rn32(np.array([x, up], np.float32))
+    assert np.isfinite(got[0]) and np.isinf(got[1])
+
+
+def test_router_sigmoid_closed_forms():
+    """1 / (1 + e^-l) with each step rounded once: exact values at 0 and in
+    the saturated tails, monotone over a dense sweep, within three float32
+    ulps of the exact logistic (scipy's float64 expit: three roundings of at
+    most half an ulp each, relative to a result that may sit at the bottom
+    of its binade), and the reflection sigma(l) + sigma(-l) = 1 to two ulps."""
+    s = omoe.router_sigmoid
+    assert s(np.float32(0.0)) == np.float32(0.5)
+    assert np.all(s(np.array([17.0, 30.0, 1e30], np.float32)) == 1.0)
+    assert np.all(s(np.array([-89.0, -1e30], np.float32)) == 0.0)
+    sweep = np.sort(np.random.default_rng(4).uniform(-40, 40, 200001).astype(np.float32))
+    sig = s(sweep)
+    assert np.all(np.diff(sig) >= 0)
+    ref = expit(sweep.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    tiny = ref > 1e-30
+    assert np.all(np.abs(sig - ref)[tiny] <= 3 * ulp[tiny])
+    mid = np.abs(sweep) < 15
+    assert np.all(np.abs(sig[mid] + s(-sweep[mid]) - 1.0) <= 2 * np.spacing(np.float32(1.0)))
+
+
+# ---------------------------------------------------------------------------
 # routes, tile maps, packing
 # ---------------------------------------------------------------------------
 
