@@ -48,6 +48,10 @@ SIGNATURES = {
                                  _i64, _i64, _i, _i, _i, _i, _p]),
     "akas_fp8_expert_swiglu": (_i, [_p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _p,
                                     _i64, _i, _i, _i64, _i64, _i, _i, _i, _i, _i, _p]),
+    "akas_expert_swiglu": (_i, [_p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _i64, _i,
+                                _i, _i64, _i64, _i, _i, _i, _i, _i, _p]),
+    "akas_expert_pair_partial": (_i, [_p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _i64,
+                                      _i, _i, _i64, _i64, _i, _i, _p]),
     "akas_swiglu_experts": (_i, [_p, _p, _i, _p, _i, _i64, _i, _i64, _i, _i, _i, _p]),
     "akas_moe_combine": (_i, [_p, _i, _p, _p, _i, _p, _i, _p, _i64, _i, _i64, _p]),
     "akas_routed_combine": (_i, [_p, _i, _p, _p, _p, _i64, _i, _i64, _p]),

@@ -218,23 +218,6 @@ AKAS_DEV v8i as_fragment(const RawFragment& f) {
   return v;
 }
 
-template <int DT>
-AKAS_DEV void store_out4(void* out, int64_t i, const v4f& v) {
-  if constexpr (DT == AKAS_DTYPE_F32) {
-    *reinterpret_cast<v4f*>(reinterpret_cast<float*>(out) + i) = v;
-  } else {
-    uint2 q;
-    if constexpr (DT == AKAS_DTYPE_BF16) {
-      q.x = f32x2_to_bf16x2(v[0], v[1]);
-      q.y = f32x2_to_bf16x2(v[2], v[3]);
-    } else {
-      q.x = f32_to_f16_bits(v[0]) | (f32_to_f16_bits(v[1]) << 16);
-      q.y = f32_to_f16_bits(v[2]) | (f32_to_f16_bits(v[3]) << 16);
-    }
-    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + i) = q;
-  }
-}
-
 constexpr int kSplitQuarters = 4;  // k-split of a workgroup: four waves
 constexpr int kBufferDword3 = 0x00020000;  // buffer resource word 3 (raw 32-bit data)
 constexpr int kSplitKbw = 4;       // k-blocks per wave: 2048-deep partitions

@@ -155,4 +155,23 @@ AKAS_DEV void store_out(void* out, int64_t i, float v) {
     reinterpret_cast<uint16_t*>(out)[i] = (uint16_t)f32_to_f16_bits(v);
 }
 
+// Four consecutive output elements in one vector store (16 bytes of f32, 8
+// of f16/bf16); `i` must keep the store aligned.
+template <int DT>
+AKAS_DEV void store_out4(void* out, int64_t i, const v4f& v) {
+  if constexpr (DT == AKAS_DTYPE_F32) {
+    *reinterpret_cast<v4f*>(reinterpret_cast<float*>(out) + i) = v;
+  } else {
+    uint2 q;
+    if constexpr (DT == AKAS_DTYPE_BF16) {
+      q.x = f32x2_to_bf16x2(v[0], v[1]);
+      q.y = f32x2_to_bf16x2(v[2], v[3]);
+    } else {
+      q.x = f32_to_f16_bits(v[0]) | (f32_to_f16_bits(v[1]) << 16);
+      q.y = f32_to_f16_bits(v[2]) | (f32_to_f16_bits(v[3]) << 16);
+    }
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + i) = q;
+  }
+}
+
 }  // namespace akas

@@ -1,7 +1,10 @@
 // Grouped (per-expert) block-scaled FP8 GEMMs for gfx950:
-//   expert_partial     -- gathered rows x expert weights, scattered to (row, rank)
-//   fp8_expert_swiglu  -- gate and up products in one tile, SwiGLU, and
-//                         per-128-column FP8 re-quantization in the epilogue.
+//   expert_partial       -- gathered rows x expert weights, scattered to (row, rank)
+//   fp8_expert_swiglu    -- gate and up products in one tile, SwiGLU, and
+//                           per-128-column FP8 re-quantization in the epilogue
+//   expert_swiglu        -- the same paired tile and SwiGLU, stored unquantized
+//   expert_pair_partial  -- the paired tile's gate and up f32 partials per
+//                           K-partition, into two outputs
 //
 // Work items are (expert, BM-row tile, BN-column block).  Each workgroup finds
 // its (expert, tile) from a wave-level prefix over ceil(counts[e]/BM), the same
@@ -31,6 +34,7 @@ struct ExpertArgs {
   const int32_t* routes;   // [E, r]
   const int32_t* offsets;  // expert_offsets (packed input/output)
   void* out;
+  void* out2;          // up partials (expert_pair_partial)
   float* out_scales;
   int r, top, E, N, K;
   int x_rows;    // rows addressable in x / as (gathered rows are clamped to it)
@@ -100,14 +104,22 @@ AKAS_DEV int source_row(const ExpertArgs& p, int e, int idx) {
   return row < 0 ? 0 : (row >= p.x_rows ? p.x_rows - 1 : row);
 }
 
-// MODE 0: expert_partial (scatter f32/f16/bf16 to out[route][part][col]).
-// MODE 1: fp8_expert_swiglu (B tile = 16-row gate/up tiles interleaved).
+// Epilogue modes of the grouped kernels.  Modes 1-3 share the paired tile:
+// B holds 16-row gate and up tiles interleaved, so each lane ends with the
+// gate and the up value of the same (row, column).
+enum ExpertMode {
+  kPartial = 0,      // expert_partial: out[route][part][col] in OUT
+  kSwigluFp8 = 1,    // fp8_expert_swiglu: SwiGLU, per-128 FP8 codes + scales
+  kSwiglu = 2,       // expert_swiglu: SwiGLU stored in OUT
+  kPairPartial = 3,  // expert_pair_partial: gate -> out, up -> out2, f32 per part
+};
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, int MODE, int OUT, int SDT>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(ExpertArgs p) {
   constexpr int THREADS = 64 * WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int MT = WM / 16, NT = WN / 16;
-  constexpr bool PAIRED = MODE == 1;
+  constexpr bool PAIRED = MODE != kPartial;
   static_assert(!PAIRED || (BN == 256 && NT % 2 == 0), "paired tiles hold 128 gate + 128 up");
   static_assert(PAIRED || 128 % WN == 0, "a wave's columns must stay inside one scale block");
   using Plan = StagePlan<BM, BN, THREADS>;
@@ -121,7 +133,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
   __shared__ __attribute__((aligned(16))) float lds_as[NSTAGE][BM];
   __shared__ int rows_src[BM];
   __shared__ int rows_dst[BM];
-  __shared__ float row_max[PAIRED ? WAVES_N : 1][PAIRED ? BM : 1];
+  __shared__ float row_max[MODE == kSwigluFp8 ? WAVES_N : 1][MODE == kSwigluFp8 ? BM : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // Tiles walked fastest, so the dead tiles past each column block's live
@@ -256,6 +268,40 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
                          acc.t[i][j][e4]);
         }
       }
+  } else if constexpr (MODE == kPairPartial) {
+    const int64_t rstride = (int64_t)p.parts * p.N;
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int dst = rows_dst[a_row0 + 16 * i + 4 * (lane >> 4) + e4];
+        if (dst < 0) continue;
+#pragma unroll
+        for (int j = 0; j < NT / 2; ++j) {
+          const int64_t at = (int64_t)dst * rstride + (int64_t)part * p.N + wcol + 16 * j + (lane & 15);
+          reinterpret_cast<float*>(p.out)[at] = acc.t[i][2 * j][e4];
+          reinterpret_cast<float*>(p.out2)[at] = acc.t[i][2 * j + 1][e4];
+        }
+      }
+  } else if constexpr (MODE == kSwiglu) {
+    with_dtype(p.prod_dtype, [&](auto PD) __attribute__((always_inline)) {
+      with_dtype(p.act_dtype, [&](auto AD) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4) {
+            const int dst = rows_dst[a_row0 + 16 * i + 4 * (lane >> 4) + e4];
+            if (dst < 0) continue;
+#pragma unroll
+            for (int j = 0; j < NT / 2; ++j) {
+              const float g = round_t<decltype(PD)::value>(acc.t[i][2 * j][e4]);
+              const float u = round_t<decltype(PD)::value>(acc.t[i][2 * j + 1][e4]);
+              const float a = round_t<decltype(AD)::value>(swiglu_elem(g, u));
+              store_out<OUT>(p.out, (int64_t)dst * p.N + wcol + 16 * j + (lane & 15), a);
+            }
+          }
+      });
+    });
   } else {
     // SwiGLU on (gate, up) pairs held by the same lane, then row max over the
     // 128 activation columns of the tile (16 lanes x NT/2 tiles x WAVES_N).
@@ -326,11 +372,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
 // ---------------------------------------------------------------------------
 template <int MODE, int OUT, int SDT>
 __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) {
-  constexpr bool PAIRED = MODE == 1;
+  constexpr bool PAIRED = MODE != kPartial;
   constexpr int BM = dma::BM;
   __shared__ int rows_src[BM];
   __shared__ int rows_dst[BM];
-  __shared__ float row_max[PAIRED ? 2 : 1][PAIRED ? BM : 1];
+  __shared__ float row_max[MODE == kSwigluFp8 ? 2 : 1][MODE == kSwigluFp8 ? BM : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -403,6 +449,45 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
     dma::store_tile<OUT>(
         acc, p.out, wave, lane, [&](int r) { return rows_dst[a_row0 + r] >= 0; },
         [&](int r) { return (int64_t)rows_dst[a_row0 + r] * rstride + (int64_t)part * p.N + wcol; });
+  } else if constexpr (MODE == kPairPartial) {
+    // Lane l holds, for m-tile i and column group c (0..3), gate in n-tile
+    // 2c and up in n-tile 2c+1 of row a_row0 + 16i + l%16 at output columns
+    // wcol + 16c + 4*(l/16) + 0..3: one 16-byte store into each output.
+    const int64_t rstride = (int64_t)p.parts * p.N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int dst = rows_dst[a_row0 + 16 * i + (lane & 15)];
+      if (dst < 0) continue;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int64_t at = (int64_t)dst * rstride + (int64_t)part * p.N + wcol + 16 * c + 4 * (lane >> 4);
+        *reinterpret_cast<v4f*>(reinterpret_cast<float*>(p.out) + at) = acc.t[i][2 * c];
+        *reinterpret_cast<v4f*>(reinterpret_cast<float*>(p.out2) + at) = acc.t[i][2 * c + 1];
+      }
+    }
+  } else if constexpr (MODE == kSwiglu) {
+    // Lane layout as above; SwiGLU of each (gate, up) pair, four adjacent
+    // output columns per store.
+    with_dtype(p.prod_dtype, [&](auto PD) __attribute__((always_inline)) {
+      with_dtype(p.act_dtype, [&](auto AD) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int dst = rows_dst[a_row0 + 16 * i + (lane & 15)];
+          if (dst < 0) continue;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            v4f a;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float g = round_t<decltype(PD)::value>(acc.t[i][2 * c][q]);
+              const float u = round_t<decltype(PD)::value>(acc.t[i][2 * c + 1][q]);
+              a[q] = round_t<decltype(AD)::value>(swiglu_elem(g, u));
+            }
+            store_out4<OUT>(p.out, (int64_t)dst * p.N + wcol + 16 * c + 4 * (lane >> 4), a);
+          }
+        }
+      });
+    });
   } else {
     // Lane l holds, for m-tile i and column group c (0..3), gate in n-tile
     // 2c and up in n-tile 2c+1 of row a_row0 + 16i + l%16 at output columns
@@ -514,7 +599,7 @@ int64_t capacity_tiles(int64_t r, int64_t top, int64_t experts, int64_t bm) {
 template <int BM, int BN, int WMW, int WNW, int MODE, int OUT>
 static void launch_expert(ExpertArgs a, hipStream_t s) {
   a.max_tiles = (int)capacity_tiles(a.r, a.top, a.E, BM);
-  a.tiles_n = MODE == 1 ? a.N / (BN / 2) : a.N / BN;
+  a.tiles_n = MODE != kPartial ? a.N / (BN / 2) : a.N / BN;
   dim3 grid((unsigned)(a.max_tiles * a.tiles_n), (unsigned)a.parts);
   if (a.ws_dtype == AKAS_DTYPE_F32)
     expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_F32><<<grid, 64 * WMW * WNW, 0, s>>>(a);
@@ -525,7 +610,7 @@ static void launch_expert(ExpertArgs a, hipStream_t s) {
 template <int MODE, int OUT>
 static void launch_expert_dma(ExpertArgs a, hipStream_t s) {
   a.max_tiles = (int)capacity_tiles(a.r, a.top, a.E, dma::BM);
-  a.tiles_n = MODE == 1 ? a.N / (dma::BN / 2) : a.N / dma::BN;
+  a.tiles_n = MODE != kPartial ? a.N / (dma::BN / 2) : a.N / dma::BN;
   dim3 grid((unsigned)(a.max_tiles * a.tiles_n), (unsigned)a.parts);
   if (a.ws_dtype == AKAS_DTYPE_F32)
     expert_dma_kernel<MODE, OUT, AKAS_DTYPE_F32><<<grid, dma::THREADS, 0, s>>>(a);
@@ -552,14 +637,22 @@ static void launch_partial(const ExpertArgs& a, hipStream_t s) {
     launch_expert<128, 128, 2, 2, 0, OUT>(a, s);
 }
 
-static void launch_swiglu(const ExpertArgs& a, hipStream_t s) {
+// The paired kernels (modes 1-3), row tile by the mean rows per expert as
+// for expert_partial.
+template <int MODE, int OUT>
+static void launch_paired(const ExpertArgs& a, hipStream_t s) {
   const int64_t mean = (int64_t)a.r * a.top / a.E;
+  const bool aligned = MODE != kPairPartial || reinterpret_cast<uintptr_t>(a.out2) % 16 == 0;
   if (mean <= 48)
-    launch_expert<32, 256, 1, 4, 1, AKAS_DTYPE_F32>(a, s);
-  else if (expert_dma_fits(a, mean, dma::BN / 2))
-    launch_expert_dma<1, AKAS_DTYPE_F32>(a, s);
+    launch_expert<32, 256, 1, 4, MODE, OUT>(a, s);
+  else if (aligned && expert_dma_fits(a, mean, dma::BN / 2))
+    launch_expert_dma<MODE, OUT>(a, s);
   else
-    launch_expert<128, 256, 2, 4, 1, AKAS_DTYPE_F32>(a, s);
+    launch_expert<128, 256, 2, 4, MODE, OUT>(a, s);
+}
+
+static void launch_swiglu(const ExpertArgs& a, hipStream_t s) {
+  launch_paired<kSwigluFp8, AKAS_DTYPE_F32>(a, s);
 }
 
 static inline bool float_dtype(int d) {
@@ -661,6 +754,81 @@ extern "C" int akas_fp8_expert_swiglu(const uint8_t* x, const float* activation_
   a.parts = 1; a.kb_per_part = (int)(k / kBlock);
   a.ws_dtype = scale_dtype; a.prod_dtype = product_dtype; a.act_dtype = activation_dtype;
   launch_swiglu(a, reinterpret_cast<hipStream_t>(stream));
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_expert_swiglu(const uint8_t* x, const float* activation_scales,
+                                  const uint8_t* w, const void* w_scales, const uint8_t* w2,
+                                  const void* w2_scales, int scale_dtype, const int32_t* counts,
+                                  const int32_t* routes, const int32_t* tile_experts,
+                                  const int32_t* tile_offsets, const int32_t* expert_offsets,
+                                  void* out, int out_dtype, int64_t r, int top, int experts,
+                                  int64_t o, int64_t k, int product_dtype, int activation_dtype,
+                                  int max_block_m, int packed_input, int packed_output,
+                                  void* stream) {
+  (void)tile_experts;
+  (void)tile_offsets;
+  const int64_t x_rows =
+      packed_input ? capacity_tiles(r, top, experts, max_block_m) * max_block_m : r;
+  int st = check_common(r, top, experts, o, k, max_block_m, packed_input, x_rows);
+  if (st != AKAS_OK) return st;
+  if (packed_output && !packed_input) return AKAS_ERR_GEOMETRY;
+  if (!float_dtype(product_dtype) || !float_dtype(activation_dtype) || !float_dtype(out_dtype) ||
+      !scale_dtype_ok(scale_dtype))
+    return AKAS_ERR_DTYPE;
+  if (r == 0) return AKAS_OK;
+  if (!x || !activation_scales || !w || !w_scales || !w2 || !w2_scales || !counts || !routes ||
+      !out)
+    return AKAS_ERR_NULL;
+  if ((packed_input || packed_output) && !expert_offsets) return AKAS_ERR_NULL;
+  ExpertArgs a{};
+  a.x = x; a.as = activation_scales; a.w = w; a.ws = w_scales; a.w2 = w2; a.ws2 = w2_scales;
+  a.counts = counts; a.routes = routes; a.offsets = expert_offsets; a.out = out;
+  a.r = (int)r; a.top = top; a.E = experts; a.N = (int)o; a.K = (int)k;
+  a.routed = 0; a.packed_in = packed_input; a.packed_out = packed_output;
+  a.x_rows = (int)x_rows;
+  a.out_rows = (int)(packed_output ? capacity_tiles(r, top, experts, max_block_m) * max_block_m
+                                   : r * top);
+  a.parts = 1; a.kb_per_part = (int)(k / kBlock);
+  a.ws_dtype = scale_dtype; a.prod_dtype = product_dtype; a.act_dtype = activation_dtype;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (out_dtype) {
+    case AKAS_DTYPE_F32: launch_paired<kSwiglu, AKAS_DTYPE_F32>(a, s); break;
+    case AKAS_DTYPE_BF16: launch_paired<kSwiglu, AKAS_DTYPE_BF16>(a, s); break;
+    default: launch_paired<kSwiglu, AKAS_DTYPE_F16>(a, s);
+  }
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_expert_pair_partial(const uint8_t* x, const float* activation_scales,
+                                        const uint8_t* w, const void* w_scales, const uint8_t* w2,
+                                        const void* w2_scales, int scale_dtype,
+                                        const int32_t* counts, const int32_t* routes,
+                                        const int32_t* tile_experts, const int32_t* tile_offsets,
+                                        float* gate, float* up, int64_t r, int top, int experts,
+                                        int64_t o, int64_t k, int partitions, int max_block_m,
+                                        void* stream) {
+  (void)tile_experts;
+  (void)tile_offsets;
+  int st = check_common(r, top, experts, o, k, max_block_m, 0, r);
+  if (st != AKAS_OK) return st;
+  if (partitions < 1 || (k / kBlock) % partitions) return AKAS_ERR_GEOMETRY;
+  if (!scale_dtype_ok(scale_dtype)) return AKAS_ERR_DTYPE;
+  if (r == 0) return AKAS_OK;
+  if (!x || !activation_scales || !w || !w_scales || !w2 || !w2_scales || !counts || !routes ||
+      !gate || !up)
+    return AKAS_ERR_NULL;
+  ExpertArgs a{};
+  a.x = x; a.as = activation_scales; a.w = w; a.ws = w_scales; a.w2 = w2; a.ws2 = w2_scales;
+  a.counts = counts; a.routes = routes; a.out = gate; a.out2 = up;
+  a.r = (int)r; a.top = top; a.E = experts; a.N = (int)o; a.K = (int)k;
+  a.routed = 0; a.packed_in = 0; a.packed_out = 0;
+  a.x_rows = (int)r; a.out_rows = (int)(r * top);
+  a.parts = partitions; a.kb_per_part = (int)(k / kBlock / partitions);
+  a.ws_dtype = scale_dtype;
+  launch_paired<kPairPartial, AKAS_DTYPE_F32>(a, reinterpret_cast<hipStream_t>(stream));
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }

@@ -87,10 +87,15 @@ class SharedExpert:
 
 
 def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed, max_block_m,
-                          product_dtype, activation_dtype, contribution_dtype, quantized=None):
+                          product_dtype, activation_dtype, contribution_dtype, quantized=None,
+                          partitions=1):
     """Routes, FP8 activations and the grouped expert products:
     ``[T, top, H]`` contributions in ``contribution_dtype``.  ``quantized``:
-    x's codes and scales when the caller made them already."""
+    x's codes and scales when the caller made them already.  ``partitions``
+    > 1 splits every expert product over K as the reference's partitions
+    policy does (src/akas/ops/moe/definition.py:796-948): gate/up through
+    expert_pair_partial -> swiglu_experts -> quantize, the down projection
+    through expert_partial(partitions) -> expert_merge."""
     rows, hidden = x.shape
     experts = weights.experts
     counts, routes = ops.quantized_routes(ids, active, experts=experts)
@@ -105,6 +110,17 @@ def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed,
     # written -- active rows route all `top` ranks, the expert products read
     # only routed entries and the combine skips inactive rows.
     width = weights.width
+    if partitions > 1:
+        gate, up = ops.expert_pair_partial(codes, scales, weights.w1, weights.s1, weights.w3,
+                                           weights.s3, counts, routes, tile_experts, tile_rows,
+                                           partitions=partitions, **common)
+        activated = ops.swiglu_experts(gate, up, round_inputs=True, round_dtype=product_dtype,
+                                       output_dtype=activation_dtype)
+        act, act_scales = ops.quantize(activated, top=top)
+        partial = ops.expert_partial(act, act_scales, weights.w2, weights.s2, counts, routes,
+                                     tile_experts, tile_rows, routed_input=True,
+                                     partitions=partitions, **common)
+        return ops.expert_merge(partial, output_dtype=contribution_dtype), counts, routes
     if fused_swiglu:
         act_rows = ((ops.tile_capacity(rows, top, experts, max_block_m) * max_block_m,) if packed
                     else (rows, top))
@@ -136,13 +152,23 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
                router="biased_softmax_router", scale=1.0, normalize=True, fused_swiglu=True,
                packed=False, max_block_m=64, product_dtype=torch.float32,
                activation_dtype=torch.float32, contribution_dtype=torch.float32,
-               return_routing=False):
-    """One routed MoE feed-forward: ``x [T, H]`` (f32/f16/bf16) -> f32 ``[T, H]``."""
+               partitions=1, partition_maximum_rows=None, return_routing=False):
+    """One routed MoE feed-forward: ``x [T, H]`` (f32/f16/bf16) -> f32 ``[T, H]``.
+
+    ``partitions`` > 1 applies the reference's K-partition policy to batches
+    of at most ``partition_maximum_rows`` rows (all batches when None), as
+    its one-row decode seed does (``partitions: 2, partition_maximum_rows:
+    1``, src/akas/ops/moe/definition.py:637-652).
+    """
     if router not in ("biased_router", "biased_softmax_router"):
         raise ValueError("unknown routed expert scoring")
     if packed and not fused_swiglu:
         raise ValueError("packing requires the fused SwiGLU pair kernel")
     rows = x.shape[0]
+    if partition_maximum_rows is not None and rows > partition_maximum_rows:
+        partitions = 1
+    if partitions > 1 and packed:
+        raise ValueError("the partitions policy applies to compact (unpacked) experts")
     if active is None:
         active = _all_active(rows, x.device)
     quantized = None
@@ -161,7 +187,7 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
         x, ids, active, weights, top=top, fused_swiglu=fused_swiglu, packed=packed,
         max_block_m=max_block_m, product_dtype=product_dtype,
         activation_dtype=activation_dtype, contribution_dtype=contribution_dtype,
-        quantized=quantized)
+        quantized=quantized, partitions=partitions)
     out = ops.routed_combine(contributions, probability, active)
     if return_routing:
         return out, dict(ids=ids, weights=probability, counts=counts, routes=routes)

@@ -576,6 +576,72 @@ def fp8_expert_swiglu(x, activation_scales, w, scales, w2, scales2, counts, rout
     return out, output_scales
 
 
+def _paired_inputs(x, activation_scales, w, scales, w2, scales2, counts, routes, r):
+    _need(x, "x", torch.uint8)
+    _need(w, "w", torch.uint8)
+    _need(w2, "w2", torch.uint8, tuple(w.shape))
+    experts, o, k = w.shape
+    sshape = (experts, (o + BLOCK - 1) // BLOCK, k // BLOCK)
+    _need(scales, "scales", _SCALES, sshape)
+    _need(scales2, "scales2", scales.dtype, sshape)
+    _need(counts, "counts", torch.int32, (experts,))
+    _need(routes, "routes", torch.int32, (experts, r))
+    _need(activation_scales, "activation_scales", torch.float32, (*x.shape[:-1], k // BLOCK))
+    return experts, o, k
+
+
+def expert_swiglu(x, activation_scales, w, scales, w2, scales2, counts, routes,
+                  tile_experts=None, tile_offsets=None, expert_offsets=None, *, r, top,
+                  product_dtype=torch.float32, activation_dtype=torch.float32,
+                  output_dtype=torch.float32, max_block_m=64, packed_input=False,
+                  packed_output=False, out=None):
+    """``expert_swiglu`` (FP8 paired): gate and up products of one tile,
+    SwiGLU, stored unquantized in ``output_dtype`` -- ``[r, top, o]``, or
+    packed ``[cap*A, o]`` with ``packed_output``.  Bit-identical to
+    ``expert_partial`` x2 -> ``swiglu_experts`` with the same dtypes
+    (src/akas/ops/moe/cuda.py:1531-1534)."""
+    experts, o, k = _paired_inputs(x, activation_scales, w, scales, w2, scales2, counts, routes, r)
+    if (packed_input or packed_output) and expert_offsets is None:
+        raise ValueError("packed experts require expert_offsets")
+    if packed_output and not packed_input:
+        raise ValueError("packed expert output requires a packed paired projection")
+    oshape = ((tile_capacity(r, top, experts, max_block_m) * max_block_m, o) if packed_output
+              else (r, top, o))
+    out = _out(out, "out", oshape, _torch_dtype(output_dtype), x)
+    check(_lib.load().akas_expert_swiglu(
+        _ptr(x), _ptr(activation_scales), _ptr(w), _ptr(scales), _ptr(w2), _ptr(scales2),
+        _dt(scales.dtype), _ptr(counts), _ptr(routes), _ptr(tile_experts), _ptr(tile_offsets),
+        _ptr(expert_offsets), _ptr(out), _dt(out.dtype), r, top, experts, o, k,
+        _dt(product_dtype), _dt(activation_dtype), max_block_m, int(bool(packed_input)),
+        int(bool(packed_output)), _stream()), "expert_swiglu")
+    return out
+
+
+def expert_pair_partial(x, activation_scales, w, scales, w2, scales2, counts, routes,
+                        tile_experts=None, tile_offsets=None, *, r, top, partitions=1,
+                        max_block_m=64, gate=None, up=None):
+    """``expert_pair_partial``: the gate (``w``) and up (``w2``) products of
+    one paired tile as f32 K-partition partials, ``(gate, up)`` each
+    ``[r, top, partitions, o]``; only routed entries are written
+    (src/akas/ops/moe/cuda.py:1537-1542, OutputABI ``("gate", "up")``)."""
+    experts, o, k = _paired_inputs(x, activation_scales, w, scales, w2, scales2, counts, routes, r)
+    if x.dim() != 2 or x.shape[0] != r:
+        raise ValueError("paired partial input must be [r, k] codes")
+    if partitions < 1 or (k // BLOCK) % partitions:
+        raise ValueError("partitions must divide the k-blocks")
+    shape = (r, top, partitions, o)
+    gate = torch.zeros(shape, dtype=torch.float32, device=x.device) if gate is None else gate
+    up = torch.zeros(shape, dtype=torch.float32, device=x.device) if up is None else up
+    _need(gate, "gate", torch.float32, shape)
+    _need(up, "up", torch.float32, shape)
+    check(_lib.load().akas_expert_pair_partial(
+        _ptr(x), _ptr(activation_scales), _ptr(w), _ptr(scales), _ptr(w2), _ptr(scales2),
+        _dt(scales.dtype), _ptr(counts), _ptr(routes), _ptr(tile_experts), _ptr(tile_offsets),
+        _ptr(gate), _ptr(up), r, top, experts, o, k, partitions, max_block_m, _stream()),
+        "expert_pair_partial")
+    return gate, up
+
+
 def swiglu_experts(g, u, *, round_inputs=False, round_dtype=torch.float32,
                    output_dtype=torch.float32, out=None):
     """``swiglu_experts``: ``g / (1 + exp(-g)) * u`` on ``[r, top, (parts,) c]``.

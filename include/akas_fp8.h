@@ -349,6 +349,48 @@ int akas_fp8_expert_swiglu(const uint8_t* x, const float* activation_scales, con
                            int packed_input, int packed_output, void* stream);
 
 /*
+ * expert_swiglu(r, top, experts, o, k[, product_dtype, activation_dtype,
+ * output_dtype, max_block_m, packed_input, packed_output]), the FP8 paired
+ * form: x, activation_scales, w, scales, w2, scales2, counts, routes,
+ * tile_experts, tile_offsets[, expert_offsets] -> out.
+ * Replaces src/akas/ops/moe/cuda.py:1531-1534 (fp8_paired_swiglu, kind
+ * registered at src/akas/ops/moe/definition.py:2138-2188, OutputABI (-1,)).
+ * fp8_expert_swiglu without the re-quantization: g, u rounded to
+ * product_dtype, a = silu(g)*u rounded to activation_dtype, stored in
+ * out_dtype: out [r, top, o] (or packed [cap*A, o]).  Bit-identical to
+ * expert_partial x2 -> swiglu_experts with the same dtypes.
+ */
+int akas_expert_swiglu(const uint8_t* x, const float* activation_scales, const uint8_t* w,
+                       const void* w_scales, const uint8_t* w2, const void* w2_scales,
+                       int scale_dtype, const int32_t* counts, const int32_t* routes,
+                       const int32_t* tile_experts, const int32_t* tile_offsets,
+                       const int32_t* expert_offsets, void* out, int out_dtype, int64_t r, int top,
+                       int experts, int64_t o, int64_t k, int product_dtype,
+                       int activation_dtype, int max_block_m, int packed_input, int packed_output,
+                       void* stream);
+
+/*
+ * expert_pair_partial(r, top, experts, o, k, partitions[, max_block_m]):
+ * x, activation_scales, w, scales, w2, scales2, counts, routes, tile_experts,
+ * tile_offsets -> gate, up.
+ * Replaces src/akas/ops/moe/cuda.py:1537-1542 (paired_partial, kind
+ * registered at src/akas/ops/moe/definition.py:2423-2462, OutputABI (-2, -1)
+ * ("gate", "up")); the partitions policy of fp8_expert_swiglu
+ * (definition.py:796-948) feeds its outputs to swiglu_experts.
+ * gate, up f32 [r, top, partitions, o]: the expert_partial products of w and
+ * of w2 over k-partition p (k-blocks [p*k/(128*partitions), ...)), each
+ * bit-identical to expert_partial on that weight; only routed entries are
+ * written.  x codes [r, k] (not routed), o % 128 == 0,
+ * (k / 128) % partitions == 0.
+ */
+int akas_expert_pair_partial(const uint8_t* x, const float* activation_scales, const uint8_t* w,
+                             const void* w_scales, const uint8_t* w2, const void* w2_scales,
+                             int scale_dtype, const int32_t* counts, const int32_t* routes,
+                             const int32_t* tile_experts, const int32_t* tile_offsets,
+                             float* gate, float* up, int64_t r, int top, int experts, int64_t o,
+                             int64_t k, int partitions, int max_block_m, void* stream);
+
+/*
  * swiglu_experts(r, top, c, expert_rows, input_dtype, output_dtype
  * [, round_inputs, round_dtype, partitions]): g, u -> out.
  * Replaces src/akas/ops/activation/kernel.py:28-88.  g, u

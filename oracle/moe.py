@@ -377,6 +377,58 @@ def swiglu_experts(gate, up, round_inputs=False, round_dtype="float32", output_d
     return round_to(out, output_dtype)
 
 
+def _paired_activations(x, activation_scales, w, scales, w2, scales2, counts, routes, top,
+                        product_dtype, activation_dtype):
+    """Per live expert: ``(owners, ranks, a)`` with ``g, u`` the float32
+    products (float64 accumulation) rounded to ``product_dtype`` and
+    ``a = silu(g) * u`` rounded to ``activation_dtype``
+    (``src/akas/ops/moe/validation.py:385-404``)."""
+    x = np.asarray(x, np.uint8)
+    source = dequantize_activation(x, activation_scales).astype(np.float64)
+    for e in range(w.shape[0]):
+        c = int(counts[e])
+        if not c:
+            continue
+        owners, ranks = np.divmod(routes[e, :c].astype(np.int64), top)
+        products = [(source[owners] @ dequantize_weight(ww[e], ss[e]).T).astype(np.float32)
+                    for ww, ss in ((w, scales), (w2, scales2))]
+        g, u = (round_to(v, product_dtype) for v in products)
+        yield owners, ranks, round_to(swiglu(g, u), activation_dtype)
+
+
+def expert_swiglu(x, activation_scales, w, scales, w2, scales2, counts, routes, top,
+                  product_dtype="float32", activation_dtype="float32", output_dtype="float32"):
+    """The FP8 paired ``expert_swiglu``: gate/up products, SwiGLU, no
+    re-quantization -- ``out [r, top, o]`` holds the activation rounded to
+    ``output_dtype`` for routed entries, 0 elsewhere.  Follows
+    ``src/akas/ops/moe/validation.py:327-410`` with ``quantized_output``
+    false (``cuda.py:1531-1534``)."""
+    r = np.asarray(x).shape[0]
+    out = np.zeros((r, top, w.shape[1]), np.float32)
+    for owners, ranks, act in _paired_activations(x, activation_scales, w, scales, w2, scales2,
+                                                  counts, routes, top, product_dtype,
+                                                  activation_dtype):
+        out[owners, ranks] = round_to(act, output_dtype)
+    return out
+
+
+def expert_pair_partial(x, activation_scales, w, scales, w2, scales2, counts, routes, top,
+                        partitions=1):
+    """``(gate, up)``, each float32 ``[r, top, partitions, o]``: the
+    K-partition products of the gate weights ``w`` and the up weights ``w2``
+    for every routed (row, rank), 0 elsewhere.  Follows
+    ``src/akas/ops/moe/validation.py:299-324`` (both products evaluated
+    independently by ``_partial_products``, ``:254-296``)."""
+    r = np.asarray(x).shape[0]
+    shape = (r, top, partitions, w.shape[1])
+    pair = []
+    for ww, ss in ((w, scales), (w2, scales2)):
+        part = expert_partial(x, activation_scales, ww, ss, counts, routes, top,
+                              partitions=partitions)
+        pair.append(part.reshape(shape))
+    return tuple(pair)
+
+
 def fp8_expert_swiglu(x, activation_scales, w, scales, w2, scales2, counts, routes, top,
                       product_dtype="float32", activation_dtype="float32"):
     """Fused gate/up products, SwiGLU and per-128-group FP8 re-quantization.
@@ -389,22 +441,15 @@ def fp8_expert_swiglu(x, activation_scales, w, scales, w2, scales2, counts, rout
     tolerance (``src/akas/ops/moe/validation.py:423-432``).  Follows
     ``src/akas/ops/moe/validation.py:327-421``.
     """
-    x = np.asarray(x, np.uint8)
-    r = x.shape[0]
-    E, o, k = w.shape
+    r = np.asarray(x).shape[0]
+    o = w.shape[1]
     codes = np.zeros((r, top, o), np.uint8)
     out_scales = np.zeros((r, top, o // BLOCK), np.float32)
     normalized = np.zeros((r, top, o), np.float32)
-    source = dequantize_activation(x, activation_scales).astype(np.float64)
-    for e in range(E):
-        c = int(counts[e])
-        if not c:
-            continue
-        owners, ranks = np.divmod(routes[e, :c].astype(np.int64), top)
-        products = [(source[owners] @ dequantize_weight(ww[e], ss[e]).T).astype(np.float32)
-                    for ww, ss in ((w, scales), (w2, scales2))]
-        g, u = (round_to(v, product_dtype) for v in products)
-        act = round_to(swiglu(g, u), activation_dtype)
+    for owners, ranks, act in _paired_activations(x, activation_scales, w, scales, w2, scales2,
+                                                  counts, routes, top, product_dtype,
+                                                  activation_dtype):
+        c = owners.size
         blocks = act.reshape(c, o // BLOCK, BLOCK)
         s = group_scales(blocks)
         q = (blocks / s[..., None]).astype(np.float32)

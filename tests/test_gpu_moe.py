@@ -516,6 +516,164 @@ def test_fused_swiglu_packed_in_out(dev, pd, ad, rows, maxm):
 
 
 # ---------------------------------------------------------------------------
+# the FP8 paired kinds without re-quantization: expert_swiglu and
+# expert_pair_partial (the partitions policy's gate/up producer)
+# ---------------------------------------------------------------------------
+
+def _paired_case(rng, rows, top, experts, o, k, mult=1):
+    ids, active = pattern_routes(rows, top, experts, mult)
+    counts, routes = omoe.quantized_routes(ids, active, experts)
+    x = random_codes(rng, (rows, k))
+    w = random_codes(rng, (experts, o, k))
+    w2 = random_codes(rng, (experts, o, k))
+    xs = rng.uniform(0.0625, 0.25, (rows, k // 128)).astype(np.float32)
+    ws = ofp8.bf16_round(rng.uniform(0.0625, 0.25, (experts, o // 128, k // 128)).astype(np.float32))
+    ws2 = ofp8.bf16_round(rng.uniform(0.0625, 0.25, (experts, o // 128, k // 128)).astype(np.float32))
+    live = np.zeros((rows, top), bool)
+    for e in range(experts):
+        for route in routes[e, :counts[e]]:
+            live[route // top, route % top] = True
+    return counts, routes, x, xs, w, ws, w2, ws2, live
+
+
+# (rows, top, experts, o, k, product, activation, output dtype): 32-row,
+# 128-row and DMA-fed 256-row tiles
+EXPERT_SWIGLU_CASES = [(1, 3, 7, 128, 256, "float32", "float32", "float32"),
+                       (33, 3, 7, 256, 384, "bfloat16", "bfloat16", "bfloat16"),
+                       (257, 3, 7, 256, 384, "float16", "float32", "float16"),
+                       (256, 4, 64, 256, 512, "bfloat16", "bfloat16", "float32"),
+                       (1200, 3, 7, 256, 384, "bfloat16", "bfloat16", "bfloat16"),
+                       (900, 2, 5, 384, 256, "float32", "float32", "float16")]
+
+
+@pytest.mark.parametrize("rows,top,experts,o,k,pd,ad,od", EXPERT_SWIGLU_CASES)
+def test_expert_swiglu_matches_separate_chain_bitwise(dev, rows, top, experts, o, k, pd, ad, od):
+    """The FP8 paired expert_swiglu equals expert_partial x2 ->
+    swiglu_experts with the same dtypes, bit for bit, is within 1e-2 of the
+    oracle, and (f32 activations and output) quantizes to exactly the fused
+    fp8_expert_swiglu codes and scales."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(904)
+    counts, routes, x, xs, w, ws, w2, ws2, live = _paired_case(rng, rows, top, experts, o, k)
+    P, A, O = (getattr(torch, d) for d in (pd, ad, od))
+    args = [_t(x, dev), _t(xs, dev)]
+    weights = [_t(w, dev), _t(ws, dev), _t(w2, dev), _t(ws2, dev)]
+    cnt, rts = _t(counts, dev), _t(routes, dev)
+    out = ops.expert_swiglu(*args, *weights, cnt, rts, r=rows, top=top, product_dtype=P,
+                            activation_dtype=A, output_dtype=O)
+    gate = ops.expert_partial(*args, weights[0], weights[1], cnt, rts, r=rows, top=top,
+                              output_dtype=P)
+    up = ops.expert_partial(*args, weights[2], weights[3], cnt, rts, r=rows, top=top,
+                            output_dtype=P)
+    if ad == od:
+        sep = ops.swiglu_experts(gate, up, output_dtype=O)
+    else:  # round to the activation dtype, then to the output dtype
+        sep = ops.swiglu_experts(gate, up, output_dtype=A).to(O)
+    np.testing.assert_array_equal(_np(out)[live], _np(sep)[live])
+    exp = omoe.expert_swiglu(x, xs, w, ws, w2, ws2, counts, routes, top, pd, ad, od)
+    assert rel_fro(_np(out)[live], exp[live]) < 1e-2
+    if ad == od == "float32":
+        codes, scales = ops.fp8_expert_swiglu(*args, *weights, cnt, rts, r=rows, top=top,
+                                              product_dtype=P, activation_dtype=A)
+        qc, qs = ops.quantize(out, top=top)
+        np.testing.assert_array_equal(_np(qc)[live], _np(codes)[live])
+        np.testing.assert_array_equal(_np(qs)[live], _np(scales)[live])
+
+
+@pytest.mark.parametrize("rows,maxm", [(33, 64), (700, 128)])
+def test_expert_swiglu_packed_in_out(dev, rows, maxm):
+    """Packed input and output: each packed row holds the unpacked result of
+    its (row, rank)."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(1036)
+    top, experts, o, k = 3, 7, 256, 384
+    counts, routes, x, xs, w, ws, w2, ws2, live = _paired_case(rng, rows, top, experts, o, k, 3)
+    te, tr = omoe.expert_tile_map(counts, rows, top, maxm)
+    px, pxs, offs = omoe.expert_pack(x, xs, counts, routes, top, experts, maxm)
+    bf = torch.bfloat16
+    weights = [_t(w, dev), _t(ws, dev), _t(w2, dev), _t(ws2, dev)]
+    cnt, rts = _t(counts, dev), _t(routes, dev)
+    packed = ops.expert_swiglu(_t(px, dev), _t(pxs, dev), *weights, cnt, rts, _t(te, dev),
+                               _t(tr, dev), _t(offs, dev), r=rows, top=top, product_dtype=bf,
+                               activation_dtype=bf, output_dtype=bf, packed_input=True,
+                               packed_output=True, max_block_m=maxm)
+    flat = ops.expert_swiglu(_t(x, dev), _t(xs, dev), *weights, cnt, rts, r=rows, top=top,
+                             product_dtype=bf, activation_dtype=bf, output_dtype=bf)
+    packed, flat = _np(packed), _np(flat)
+    for e in range(experts):
+        for local, route in enumerate(routes[e, :counts[e]]):
+            row, rank = divmod(int(route), top)
+            np.testing.assert_array_equal(packed[offs[e] + local], flat[row, rank])
+
+
+# (rows, top, experts, o, k, partitions): r = 1 with two partitions (the
+# reference's seed policy for one-row decode), 32-row, 128-row and DMA tiles
+PAIR_PARTIAL_CASES = [(1, 4, 64, 256, 2048, 2), (1, 2, 5, 128, 512, 4), (33, 3, 7, 256, 384, 3),
+                      (257, 3, 7, 256, 512, 2), (1200, 3, 7, 256, 512, 2),
+                      (900, 2, 5, 384, 256, 1)]
+
+
+@pytest.mark.parametrize("rows,top,experts,o,k,parts", PAIR_PARTIAL_CASES)
+def test_expert_pair_partial_exact(dev, rows, top, experts, o, k, parts):
+    """Exact products (codes {56, 64} with sign, binary scales; the up
+    weights are the flipped gate weights, as in the reference's
+    paired_partial_validation): gate and up partials equal the oracle bit
+    for bit; unrouted entries are untouched."""
+    from akas_amd import ops
+
+    rng = np.random.default_rng(905)
+    ids, active = pattern_routes(rows, top, experts, 1)
+    counts, routes = omoe.quantized_routes(ids, active, experts)
+    x, w = exact_codes(rng, (rows, k)), exact_codes(rng, (experts, o, k))
+    xs = (2.0 ** rng.integers(-4, 2, (rows, k // 128))).astype(np.float32)
+    ws = (2.0 ** rng.integers(-4, 2, (experts, o // 128, k // 128))).astype(np.float32)
+    w2, ws2 = np.flip(w, axis=-2).copy(), np.flip(ws, axis=-1).copy()
+    gate, up = ops.expert_pair_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev),
+                                       _t(w2, dev), _t(ws2, dev), _t(counts, dev), _t(routes, dev),
+                                       r=rows, top=top, partitions=parts)
+    eg, eu = omoe.expert_pair_partial(x, xs, w, ws, w2, ws2, counts, routes, top, parts)
+    np.testing.assert_array_equal(_np(gate), eg)
+    np.testing.assert_array_equal(_np(up), eu)
+
+
+@pytest.mark.parametrize("rows,parts", [(1, 2), (40, 3), (1200, 2)])
+def test_expert_pair_partial_then_swiglu_policy(dev, rows, parts):
+    """The reference's partitions policy for fp8_expert_swiglu
+    (src/akas/ops/moe/definition.py:796-948): expert_pair_partial ->
+    swiglu_experts (partitions summed in f32) -> quantize.  Gate and up are
+    each bit-identical to expert_partial with the same partitions, and the
+    chain's codes match the oracle's fused kind within the midpoint band."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(906)
+    top, experts, o, k = 4, 8, 256, 768
+    counts, routes, x, xs, w, ws, w2, ws2, live = _paired_case(rng, rows, top, experts, o, k)
+    args = [_t(x, dev), _t(xs, dev)]
+    cnt, rts = _t(counts, dev), _t(routes, dev)
+    gate, up = ops.expert_pair_partial(*args, _t(w, dev), _t(ws, dev), _t(w2, dev), _t(ws2, dev),
+                                       cnt, rts, r=rows, top=top, partitions=parts)
+    g1 = ops.expert_partial(*args, _t(w, dev), _t(ws, dev), cnt, rts, r=rows, top=top,
+                            partitions=parts)
+    u1 = ops.expert_partial(*args, _t(w2, dev), _t(ws2, dev), cnt, rts, r=rows, top=top,
+                            partitions=parts)
+    g_np, u_np = _np(gate), _np(up)
+    if parts == 1:
+        g_np, u_np = g_np[:, :, 0], u_np[:, :, 0]
+    np.testing.assert_array_equal(g_np[live], _np(g1)[live])
+    np.testing.assert_array_equal(u_np[live], _np(u1)[live])
+    act = ops.swiglu_experts(gate, up, output_dtype=torch.float32)
+    codes, scales = ops.quantize(act, top=top)
+    oc, osc, norm = omoe.fp8_expert_swiglu(x, xs, w, ws, w2, ws2, counts, routes, top)
+    got = ofp8.dequantize_activation(_np(codes), _np(scales))[live]
+    assert rel_fro(got, ofp8.dequantize_activation(oc, osc)[live]) < 1e-2
+
+
+# ---------------------------------------------------------------------------
 # elementwise: swiglu, combine
 # ---------------------------------------------------------------------------
 
@@ -592,6 +750,35 @@ def test_routed_moe_layer(dev, rows, packed, fused):
     exp, _, _ = omoe.moe_layer(x, logits, np.zeros(E, np.float32), *bank["w1"], *bank["w3"],
                                *bank["w2"], top)
     assert rel_fro(_np(out), exp) < 1e-2
+
+
+@pytest.mark.parametrize("rows,parts", [(1, 2), (64, 2), (200, 4)])
+def test_routed_moe_layer_partitions_policy(dev, rows, parts):
+    """The block under the reference's partitions policy (gate/up through
+    expert_pair_partial -> swiglu_experts -> quantize, down through
+    expert_partial(partitions) -> expert_merge) against the layer equation;
+    with partition_maximum_rows below the batch the policy is off and the
+    result is the plain block's, bit for bit."""
+    import torch
+    from akas_amd import moe
+
+    rng = np.random.default_rng(12)
+    H, F, E, top = 512, 512, 16, 4  # both depths split into 4 partitions
+    x = bf16_normal(rng, (rows, H))
+    logits = rng.normal(0, 1, (rows, E)).astype(np.float32)
+    bank = {}
+    for name, shape in (("w1", (E, F, H)), ("w3", (E, F, H)), ("w2", (E, H, F))):
+        bank[name] = ofp8.quantize_weight_blocks(rng.normal(0, 0.05, shape).astype(np.float32))
+    wts = moe.ExpertWeights(*(_t(a, dev) for n in ("w1", "w3", "w2") for a in bank[n]))
+    xt, lt = _t(x, dev, torch.bfloat16), _t(logits, dev)
+    out = moe.routed_moe(xt, lt, None, wts, top=top, partitions=parts)
+    exp, _, _ = omoe.moe_layer(x, logits, np.zeros(E, np.float32), *bank["w1"], *bank["w3"],
+                               *bank["w2"], top)
+    assert rel_fro(_np(out), exp) < 1e-2
+    off = moe.routed_moe(xt, lt, None, wts, top=top, partitions=parts,
+                         partition_maximum_rows=rows - 1)
+    plain = moe.routed_moe(xt, lt, None, wts, top=top)
+    np.testing.assert_array_equal(_np(off), _np(plain))
 
 
 @pytest.mark.parametrize("rows,packed,fused,policy", [

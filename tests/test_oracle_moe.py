@@ -387,6 +387,68 @@ def test_fused_swiglu_against_float64_and_composition(pd, ad):
     np.testing.assert_array_equal(scales[live], sep_scales[live])
 
 
+@pytest.mark.parametrize("pd,ad,od", [("float32", "float32", "float32"),
+                                      ("bfloat16", "bfloat16", "bfloat16"),
+                                      ("float16", "float32", "float16")])
+def test_expert_swiglu_against_float64(pd, ad, od):
+    """The unquantized paired SwiGLU: on exact products, each routed entry is
+    the float64 SwiGLU of the rounded products, rounded to the activation and
+    then the output dtype (``src/akas/ops/moe/validation.py:385-410``);
+    unrouted entries stay 0; quantizing the float32 result reproduces the
+    fused kind's codes bit for bit."""
+    rng = np.random.default_rng(832)
+    rows, top, experts, o, k = 21, 2, 5, 256, 256
+    counts, routes, x, xs, w, ws = _exact_expert_case(rng, rows, top, experts, o, k, False)
+    w2 = exact_codes(rng, (experts, o, k))
+    out = omoe.expert_swiglu(x, xs, w, ws, w2, ws, counts, routes, top, pd, ad, od)
+    live = np.zeros((rows, top), bool)
+    for e in range(experts):
+        for route in routes[e, :counts[e]]:
+            row, rank = divmod(int(route), top)
+            live[row, rank] = True
+            g = ofp8.round_to(_int_products(x[row][None], xs[row][None], w[e], ws[e]).astype(np.float32), pd)
+            u = ofp8.round_to(_int_products(x[row][None], xs[row][None], w2[e], ws[e]).astype(np.float32), pd)
+            a = (g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u).astype(np.float32)
+            exp = ofp8.round_to(ofp8.round_to(a, ad), od)[0]
+            np.testing.assert_allclose(out[row, rank], exp, rtol=8e-3 if od != "float32" else 2e-6,
+                                       atol=1e-30)
+    assert not out[~live].any()
+    if od == "float32":
+        codes, scales, _ = omoe.fp8_expert_swiglu(x, xs, w, ws, w2, ws, counts, routes, top, pd, ad)
+        qc, qs = ofp8.quantize(out)
+        np.testing.assert_array_equal(qc[live], codes[live])
+        np.testing.assert_array_equal(qs[live], scales[live])
+
+
+@pytest.mark.parametrize("parts", [1, 3])
+def test_expert_pair_partial_exact(parts):
+    """Paired partials on exact products: gate and up of every routed entry
+    equal the integer brute force over each partition's k-range, the two
+    outputs differ (distinct weights), and unrouted entries stay 0."""
+    rng = np.random.default_rng(833)
+    rows, top, experts, o, k = 17, 3, 4, 128, 384
+    counts, routes, x, xs, w, ws = _exact_expert_case(rng, rows, top, experts, o, k, False)
+    w2 = np.flip(w, axis=-2).copy()
+    ws2 = np.flip(ws, axis=-1).copy()
+    gate, up = omoe.expert_pair_partial(x, xs, w, ws, w2, ws2, counts, routes, top, parts)
+    assert gate.shape == up.shape == (rows, top, parts, o)
+    span = k // parts
+    live = np.zeros((rows, top), bool)
+    for e in range(experts):
+        for route in routes[e, :counts[e]]:
+            row, rank = divmod(int(route), top)
+            live[row, rank] = True
+            for p in range(parts):
+                seg = slice(p * span, (p + 1) * span)
+                bseg = slice(p * span // 128, (p + 1) * span // 128)
+                for got, ww, ss in ((gate, w, ws), (up, w2, ws2)):
+                    exp = _int_products(x[row][None, seg], xs[row][None, bseg], ww[e][:, seg],
+                                        ss[e][:, bseg])[0]
+                    np.testing.assert_array_equal(got[row, rank, p], exp.astype(np.float32))
+    assert not gate[~live].any() and not up[~live].any()
+    assert not np.array_equal(gate[live], up[live])
+
+
 def test_swiglu_float64():
     rng = np.random.default_rng(9)
     g = rng.normal(0, 6, 5000).astype(np.float32)
