@@ -16,6 +16,10 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "akas_amd", "csrc")
 LIBDIR = os.path.join(ROOT, "akas_amd", "lib")
 LIBRARY = os.path.join(LIBDIR, "libakas_fp8.so")
+# Roofline probes (HBM streaming read, FP8 MFMA peak) for the benchmark, in a
+# library of their own: they are measurement tools, not part of the path.
+PROBE_DIR = os.path.join(CSRC, "probe")
+PROBE_LIBRARY = os.path.join(LIBDIR, "libakas_probe.so")
 OBJDIR = os.path.join(ROOT, "_build")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -41,7 +45,8 @@ def sources():
 
 
 def _compile(src):
-    obj = os.path.join(OBJDIR, os.path.basename(src)[:-4] + ".o")
+    sub = "probe_" if os.path.dirname(src) == PROBE_DIR else ""
+    obj = os.path.join(OBJDIR, sub + os.path.basename(src)[:-4] + ".o")
     cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
@@ -56,18 +61,21 @@ def build(verbose=False, jobs=None):
     os.makedirs(OBJDIR, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
     srcs = sources()
-    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2)))
+    probes = sorted(os.path.join(PROBE_DIR, f) for f in os.listdir(PROBE_DIR) if f.endswith(".hip"))
+    jobs = jobs or min(len(srcs) + len(probes), max(1, (os.cpu_count() or 2)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(_compile, srcs))
-    tmp = LIBRARY + ".tmp"
-    # -Bsymbolic-functions: calls inside the library bind to its own definitions.
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-Bsymbolic-functions", *objs, "-o", tmp]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, LIBRARY)
+        objs = list(pool.map(_compile, srcs + probes))
+    for lib, parts in ((LIBRARY, objs[:len(srcs)]), (PROBE_LIBRARY, objs[len(srcs):])):
+        tmp = lib + ".tmp"
+        # -Bsymbolic-functions: calls inside the library bind to its own definitions.
+        cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-Bsymbolic-functions",
+               *parts, "-o", tmp]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
+        os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIBRARY} from {len(srcs)} sources", file=sys.stderr)
+        print(f"built {LIBRARY} from {len(srcs)} sources and {PROBE_LIBRARY}", file=sys.stderr)
     return LIBRARY
 
 

@@ -8,18 +8,23 @@ MFMA GEMM, bf16 out) per M.  The value is whole-step algorithmic HBM bytes
 per second, ``sum_M N*K + 4*ceil(N/128)*K/128 + 2*M*K + 2*M*N`` over the
 step time.  Every step reads a different copy of the weights (more than
 512 MB of copies in rotation), so weights stream from HBM, not from the
-256 MB last-level cache.
+256 MB last-level cache.  ``--warmup W`` steps run first, then exactly
+``--steps K`` steps are timed as one replay of a HIP graph holding them.
 
-Also reported (``extras``): the prefill-shape GEMMs (M=8192), the MoE decode
-layer (T=256), the skewed MoE prefill layer (T=16384), the fused RMSNorm +
-quantizer (16384 x 2048) and the shared-expert (Qwen3.5 block-fp8) MoE block
-at decode (T=64, 256 experts, top 8), in TFLOP/s and GB/s, each block timed
-as one of four captured back to back in a graph (as a decode step graph holds
-many layers); ``roofline`` for the dominant kernel (HIP-event timing of that kernel
-alone); ``cpu_baseline`` from the oracle's C restatement on the host cores.
+Also reported: ``roofline`` for the dominant op of the step (the M=256
+``fp8_linear``, every launch it makes), ``roofline_prefill`` for the
+prefill GEMM kernel (MFMA-bound), ``ceilings`` measured by the probe library
+(streaming HBM read, FP8 MFMA), ``extras`` (the prefill GEMMs, the MoE
+decode layer, the skewed MoE prefill layer, the fused RMSNorm + quantizer
+and the shared-expert MoE block; each MoE block timed as one of four
+captured back to back in a graph, as a decode step graph holds many layers)
+and ``cpu_baseline`` (the oracle's C restatement on the host cores, per
+config).
 
     python bench.py [--steps K] [--warmup W] [--no-extras] [--no-cpu]
-    python bench.py --kernel-probe    # launches for rocprofv3 --pmc passes
+    python bench.py --kernel-probe {decode,prefill,moe_decode,moe_prefill,copy}
+                                  # launches for rocprofv3 --pmc passes
+    python bench.py --roofline-probe   # the measured ceilings alone
 """
 
 import argparse
@@ -145,6 +150,9 @@ def graph_of(torch, fn, n):
 
 
 def decode_sweep(torch, dev, steps, warmup):
+    """The headline: ``warmup`` eager steps, then exactly ``steps`` steps timed
+    as one replay of a graph that holds them (step i on weight copy
+    i % copies), with a barrier (synchronize) on both sides."""
     from akas_amd import ops
 
     wbytes = N_DEC * K_DEC
@@ -160,39 +168,49 @@ def decode_sweep(torch, dev, steps, warmup):
         for m in DECODE_M:
             ops.fp8_linear(xs[m], c, s, out=outs[m], workspace=ws)
 
-    # one graph replay = `copies` steps, each on a different weight copy
-    g = graph_of(torch, step, copies)
-    replays = max(1, math.ceil(steps / copies))
-    for _ in range(max(1, math.ceil(warmup / copies))):
-        g.replay()
+    for i in range(warmup):
+        step(i)
+    g = graph_of(torch, step, steps)
+    g.replay()  # the graph's first replay uploads it; untimed
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(replays):
-        g.replay()
+    g.replay()
     torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / (replays * copies)
+    dt = (time.perf_counter() - t0) / steps
+    del g
 
-    # per-M GEMM kernel durations (prequantized path = the same GEMM kernel)
+    # Per M: the fp8_linear op as the step runs it (every launch it makes),
+    # and the GEMM launch alone on prequantized codes; each averaged over a
+    # graph of `copies` back-to-back launches on the launching stream.
     per_m = []
     for m in DECODE_M:
+        op_ms = time_kernel_graph(torch, lambda i: ops.fp8_linear(
+            xs[m], codes[i % copies], scales[i % copies], out=outs[m], workspace=ws), copies)
         q, qs = ops.quantize(xs[m])
         ms = time_kernel_graph(torch, lambda i: ops.projection_partial(
             q, qs, codes[i % copies], scales[i % copies], out=outs[m],
             out_dtype=torch.bfloat16), copies)
-        b = gemm_kernel_bytes(m, K_DEC, N_DEC)
-        per_m.append(dict(M=m, kernel_us=round(ms * 1e3, 3), bytes=b,
-                          gbs=round(b / (ms * 1e-3) / 1e9, 1),
-                          frac_hbm=round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                          tflops=round(2 * m * K_DEC * N_DEC / (ms * 1e-3) / 1e12, 2)))
-    return dict(step_s=dt, step_bytes=step_bytes, per_m=per_m, copies=copies,
-                steps=replays * copies)
+        ob, b = dense_bytes(m, K_DEC, N_DEC), gemm_kernel_bytes(m, K_DEC, N_DEC)
+        per_m.append(dict(M=m, op_us=round(op_ms * 1e3, 3), op_bytes=ob,
+                          op_gbs=round(ob / (op_ms * 1e-3) / 1e9, 1),
+                          op_frac_hbm=round(ob / (op_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                          gemm_us=round(ms * 1e3, 3), gemm_bytes=b,
+                          gemm_gbs=round(b / (ms * 1e-3) / 1e9, 1),
+                          tflops=round(2 * m * K_DEC * N_DEC / (op_ms * 1e-3) / 1e12, 2)))
+    return dict(step_s=dt, step_bytes=step_bytes, per_m=per_m, copies=copies, steps=steps)
+
+
+PREFILL_SHAPES = ((2048, 6144), (2048, 8192), (8192, 2048))
 
 
 def prefill_gemms(torch, dev, steps):
+    """Config 3: M=8192, fused activation quantize, bf16 out.  ``op``: the
+    fp8_linear call (all its launches); ``gemm``: its GEMM launch alone, on
+    prequantized codes (the same kernel)."""
     from akas_amd import ops
 
     res = []
-    for (k, n) in ((2048, 6144), (2048, 8192), (8192, 2048)):
+    for (k, n) in PREFILL_SHAPES:
         m = 8192
         codes, scales = make_weights(torch, n, k, 1, 7 + n, dev)
         x = bf16_activations(torch, m, k, 99, dev, outliers=0.0)
@@ -210,6 +228,7 @@ def prefill_gemms(torch, dev, steps):
                         gemm_us=round(ms_gemm * 1e3, 2),
                         op_tflops=round(flops / (ms_total * 1e-3) / 1e12, 1),
                         gemm_tflops=round(flops / (ms_gemm * 1e-3) / 1e12, 1),
+                        op_frac_fp8=round(flops / (ms_total * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
                         gemm_frac_fp8=round(flops / (ms_gemm * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4)))
         del codes, scales, x, out
     return res
@@ -325,119 +344,243 @@ def _cpu_model():
     return None
 
 
-def cpu_baseline(budget_s=12.0):
-    """The oracle's C restatement of the decode sweep on the host cores."""
-    import ctypes
+def _median_time(fn, runs, budget_s):
+    """Median wall time of ``fn()`` after one warm-up run: at least ``runs``
+    runs, more while ``budget_s`` lasts (at most 50)."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < runs or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
 
+
+def _random_codes(rng, shape):
+    """Finite e4m3 codes (magnitude code <= 126, either sign): the CPU path's
+    time does not depend on the values."""
+    n = int(np.prod(shape))
+    return (np.frombuffer(rng.bytes(n), np.uint8) & np.uint8(0xFE)).reshape(shape)
+
+
+def cpu_baseline():
+    """The oracle's C restatement (oracle/cpu_ref.c, -O3 -fopenmp, f32
+    accumulation, LUT weight decode) timed on the host cores with
+    ``os.cpu_count()`` threads, per config: the decode sweep in full (the
+    headline's baseline, also on one thread as the reference's CI runs its
+    CPU checks), config 1 in full, bounded row/token samples of configs 3
+    and 5, and the MoE decode layer of config 4 in full."""
     from oracle import native
     from oracle import fp8 as ofp8
 
     lib = native.load()
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")), 16)
+    threads = os.cpu_count() or 1
+    p = native.ptr
     rng = np.random.default_rng(0)
+    per = {}
+
+    def linear_case(m, k, n, label, sample, runs=5, budget=3.0):
+        w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+        codes, scales = ofp8.quantize_weight_blocks(w)
+        x = ofp8.bf16_bits(rng.normal(0, 1, (m, k)).astype(np.float32))
+        out = np.empty((m, n), np.uint16)
+        t, count = _median_time(lambda: lib.ref_fp8_linear_bf16(
+            p(x), p(codes), p(scales), p(out), 1, m, k, n, threads), runs, budget)
+        b = dense_bytes(m, k, n)
+        per[label] = dict(ms=round(t * 1e3, 3), gbs=round(b / t / 1e9, 3),
+                          gflops=round(2 * m * k * n / t / 1e9, 2), runs=count, sample=sample)
+
+    linear_case(16, 2048, 2048, "config1_linear_m16", "full: x [16, 2048], W [2048, 2048]")
+    linear_case(256, 2048, 6144, "config3_prefill_gemm",
+                "256 of the 8192 rows of M=8192, K=2048, N=6144 (rate scales with rows)", 3)
+
+    # config 2, the headline's baseline: the full sweep
     w = rng.normal(0, 0.02, (N_DEC, K_DEC)).astype(np.float32)
     codes, scales = ofp8.quantize_weight_blocks(w)
     xs = {m: ofp8.bf16_bits(rng.normal(0, 1, (m, K_DEC)).astype(np.float32)) for m in DECODE_M}
     outs = {m: np.empty((m, N_DEC), np.uint16) for m in DECODE_M}
 
-    def sweep():
+    def sweep(nthreads):
         for m in DECODE_M:
-            lib.ref_fp8_linear_bf16(native.ptr(xs[m]), native.ptr(codes), native.ptr(scales),
-                                    native.ptr(outs[m]), 1, m, K_DEC, N_DEC, threads)
+            lib.ref_fp8_linear_bf16(p(xs[m]), p(codes), p(scales), p(outs[m]), 1, m, K_DEC, N_DEC,
+                                    nthreads)
 
-    sweep()  # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
-        t0 = time.perf_counter()
-        sweep()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    med, runs = _median_time(lambda: sweep(threads), 5, 8.0)
+    med1, _ = _median_time(lambda: sweep(1), 3, 0.0)
     step_bytes = sum(dense_bytes(m, K_DEC, N_DEC) for m in DECODE_M)
 
-    # One thread as well (the reference's CI runs its CPU checks with
-    # OMP_NUM_THREADS=1): median of 5 sweeps.
-    def sweep1():
-        for m in DECODE_M:
-            lib.ref_fp8_linear_bf16(native.ptr(xs[m]), native.ptr(codes), native.ptr(scales),
-                                    native.ptr(outs[m]), 1, m, K_DEC, N_DEC, 1)
+    # configs 4 and 5: the MoE layer (H=2048, F=1536, 64 experts, top 4)
+    H, F, E, top = 2048, 1536, 64, 4
+    w1, w3, w2 = (_random_codes(rng, sh) for sh in ((E, F, H), (E, F, H), (E, H, F)))
+    s13 = rng.uniform(2e-4, 1e-3, (E, F // 128, H // 128)).astype(np.float32)
+    s2 = rng.uniform(2e-4, 1e-3, (E, H // 128, F // 128)).astype(np.float32)
 
-    times1 = []
-    for _ in range(5):
-        t0 = time.perf_counter()
-        sweep1()
-        times1.append(time.perf_counter() - t0)
-    med1 = float(np.median(times1))
-    return dict(value=round(step_bytes / med / 1e9, 2), unit="GB/s", cores=threads,
-                kind="port", cpu_model=_cpu_model(), host_cpus=os.cpu_count(),
-                sample=f"full decode sweep (M=1,4,16,64,256; K=2048; N=6144), median of "
-                       f"{len(times)} runs, {med * 1e3:.1f} ms/sweep, oracle/cpu_ref.c -O3 "
-                       f"-fopenmp f32 accumulation",
+    def moe_case(tokens, zipf, label, sample, runs):
+        x = ofp8.bf16_bits(rng.normal(0, 1, (tokens, H)).astype(np.float32))
+        logits = rng.normal(0, 1, (tokens, E)).astype(np.float32)
+        if zipf:
+            logits += (-1.1 * np.log1p(rng.permutation(E))).astype(np.float32)[None, :]
+        out = np.empty((tokens, H), np.float32)
+        t, count = _median_time(lambda: lib.ref_moe_layer_bf16(
+            p(x), p(logits), p(w1), p(s13), p(w3), p(s13), p(w2), p(s2), p(out), tokens, H, F, E,
+            top, threads), runs, 0.0)
+        flops = 6 * F * H * tokens * top
+        per[label] = dict(ms=round(t * 1e3, 2), gflops=round(flops / t / 1e9, 2), runs=count,
+                          sample=sample)
+
+    moe_case(256, False, "config4_moe_decode", "full: T=256, all 64 experts active", 3)
+    moe_case(512, True, "config5_moe_prefill_zipf",
+             "512 of the 16384 tokens, same Zipf(1.1) logit offsets (rate scales with tokens)", 2)
+    return dict(value=round(step_bytes / med / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                cpu_model=_cpu_model(), host_cpus=os.cpu_count(),
+                sample=f"full decode sweep (M=1,4,16,64,256; K=2048; N=6144), median of {runs} "
+                       f"runs, {med * 1e3:.1f} ms/sweep, oracle/cpu_ref.c -O3 -fopenmp, f32 "
+                       f"accumulation",
                 value_1_thread=round(step_bytes / med1 / 1e9, 3),
-                sample_1_thread=f"same sweep on 1 thread, median of 5 runs, "
-                                f"{med1 * 1e3:.1f} ms/sweep")
+                sample_1_thread=f"same sweep on 1 thread, median of 3 runs, "
+                                f"{med1 * 1e3:.1f} ms/sweep",
+                per_config=per)
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_gemm_m256_counters.md")
-
-
-def measured_traffic():
-    """HBM bytes per launch of the dominant decode GEMM from the committed
-    FETCH_SIZE / WRITE_SIZE summary (calibrated against a copy of known
-    size), or None when the summary is absent."""
+def profile_value(name, key):
+    """``key: value`` from a committed profile summary under profiles/, or
+    None when the summary or the key is absent."""
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1])
-    except OSError:
+                if line.startswith(key + ":"):
+                    return float(line.split(":", 1)[1])
+    except (OSError, ValueError):
         pass
     return None
 
 
-PROBE_M = 256          # the sweep's dominant GEMM (largest kernel time)
+DECODE_COUNTERS = "decode_fp8_linear_m256_counters.md"
+PREFILL_COUNTERS = "prefill_gemm_counters.md"
+PROBE_M = 256          # the sweep's dominant op (largest time)
 PROBE_COPY_BYTES = 256 << 20
 
 
-def kernel_probe(torch, dev):
-    """Launches for hardware-counter runs: the dominant decode GEMM (M=256,
-    prequantized input, bf16 out, each launch on a different weight copy) 20
-    times, then a plain 256 MiB device copy 5 times, whose FETCH_SIZE /
-    WRITE_SIZE calibrate the counters against a known byte count."""
-    from akas_amd import ops
-
-    copies = 20
-    codes, scales = make_weights(torch, N_DEC, K_DEC, copies, 1234, dev)
-    x = bf16_activations(torch, PROBE_M, K_DEC, PROBE_M, dev)
-    q, qs = ops.quantize(x)
-    out = torch.empty((PROBE_M, N_DEC), dtype=torch.bfloat16, device=dev)
-    for i in range(copies):
-        ops.projection_partial(q, qs, codes[i], scales[i], out=out, out_dtype=torch.bfloat16)
+def _copy_calibration(torch, dev):
+    """A plain device copy of 256 MiB, five times: FETCH_SIZE / WRITE_SIZE of
+    a known byte count, to scale the counters of the probed kernels."""
     src = torch.empty(PROBE_COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps(dict(probe="decode GEMM M=256 K=2048 N=6144 x20, then 256 MiB copy x5",
-                          gemm_bytes_per_launch=gemm_kernel_bytes(PROBE_M, K_DEC, N_DEC),
-                          copy_bytes=PROBE_COPY_BYTES)))
+
+
+def kernel_probe(torch, dev, what):
+    """Launches for hardware-counter passes, then the copy calibration."""
+    from akas_amd import moe, ops
+
+    info = dict(probe=what, copy_bytes=PROBE_COPY_BYTES)
+    if what == "decode":
+        copies = 20
+        codes, scales = make_weights(torch, N_DEC, K_DEC, copies, 1234, dev)
+        x = bf16_activations(torch, PROBE_M, K_DEC, PROBE_M, dev)
+        out = torch.empty((PROBE_M, N_DEC), dtype=torch.bfloat16, device=dev)
+        ws = ops.linear_workspace(PROBE_M, K_DEC, N_DEC, dev)
+        for i in range(copies):
+            ops.fp8_linear(x, codes[i], scales[i], out=out, workspace=ws)
+        info.update(op="fp8_linear M=256 K=2048 N=6144 bf16, x20 on 20 weight copies",
+                    op_bytes=dense_bytes(PROBE_M, K_DEC, N_DEC))
+    elif what == "prefill":
+        k, n = PREFILL_SHAPES[0]
+        codes, scales = make_weights(torch, n, k, 1, 7 + n, dev)
+        x = bf16_activations(torch, 8192, k, 99, dev, outliers=0.0)
+        out = torch.empty((8192, n), dtype=torch.bfloat16, device=dev)
+        for _ in range(5):
+            ops.fp8_linear(x, codes[0], scales[0], out=out)
+        info.update(op=f"fp8_linear M=8192 K={k} N={n} bf16, x5", flops=2 * 8192 * k * n)
+    elif what in ("moe_decode", "moe_prefill"):
+        tokens, zipf = (256, False) if what == "moe_decode" else (16384, True)
+        H, F, E = 2048, 1536, 64
+        bank = {}
+        for name, (n, k) in (("w1", (F, H)), ("w3", (F, H)), ("w2", (H, F))):
+            c, sc = make_weights(torch, n, k, E, {"w1": 1, "w3": 3, "w2": 2}[name], dev)
+            bank[name] = (torch.stack(c), torch.stack(sc))
+            del c, sc
+        wts = moe.ExpertWeights(*bank["w1"], *bank["w3"], *bank["w2"])
+        rng = np.random.default_rng(0)
+        x = torch.from_numpy(rng.normal(0, 1, (tokens, H)).astype(np.float32)).to(dev).to(torch.bfloat16)
+        logits = rng.normal(0, 1, (tokens, E)).astype(np.float32)
+        if zipf:
+            logits += (-1.1 * np.log1p(rng.permutation(E))).astype(np.float32)[None, :]
+        logits = torch.from_numpy(logits).to(dev)
+        packed = tokens >= 2048
+        for _ in range(3):
+            moe.routed_moe(x, logits, None, wts, top=4, packed=packed,
+                           max_block_m=128 if packed else 64, product_dtype=torch.bfloat16,
+                           activation_dtype=torch.bfloat16, contribution_dtype=torch.bfloat16)
+        info.update(op=f"routed MoE layer T={tokens}{' zipf' if zipf else ''}, x3",
+                    flops=6 * F * H * tokens * 4)
+    elif what != "copy":
+        raise SystemExit(f"unknown kernel probe {what!r}")
+    torch.cuda.synchronize()
+    _copy_calibration(torch, dev)
+    print(json.dumps(info))
+
+
+def roofline_ceilings(torch, dev):
+    """The GPU's measured ceilings from the probe library: a streaming read
+    of 1 GiB (four times the 256 MB last-level cache) at several grid sizes,
+    and back-to-back FP8 MFMAs at 8 waves per SIMD; each the best of 5 timed
+    launches (HIP events on the launching stream)."""
+    import ctypes
+
+    from akas_amd import build
+
+    lib = ctypes.CDLL(build.PROBE_LIBRARY)
+    lib.akas_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                           ctypes.c_int, ctypes.c_void_p]
+    lib.akas_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.akas_probe_mfma_flops.argtypes = [ctypes.c_int, ctypes.c_int]
+    lib.akas_probe_mfma_flops.restype = ctypes.c_double
+    nbytes = 1 << 30
+    buf = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    best_read = (0.0, 0)
+    for blocks in (1024, 2048, 4096, 8192):
+        sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+        stream = torch.cuda.current_stream().cuda_stream
+        ms = time_kernel(torch, lambda i: lib.akas_probe_stream_read(
+            buf.data_ptr(), nbytes, sink.data_ptr(), blocks, stream), 5)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        best_read = max(best_read, (gbs, blocks))
+    del buf
+    iters, blocks = 4000, 256 * 8
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    ms = time_kernel(torch, lambda i: lib.akas_probe_mfma(sink.data_ptr(), iters, blocks, stream), 5)
+    tflops = lib.akas_probe_mfma_flops(iters, blocks) / (ms * 1e-3) / 1e12
+    return dict(hbm_read_gbs=round(best_read[0], 1), hbm_read_grid=best_read[1],
+                hbm_read_frac_of_peak=round(best_read[0] / HBM_PEAK_GBS, 4),
+                mfma_fp8_tflops=round(tflops, 1),
+                mfma_fp8_frac_of_peak=round(tflops / FP8_PEAK_TFLOPS, 4),
+                source="akas_amd/csrc/probe/roofline.hip")
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--kernel-probe", action="store_true",
-                    help="only launch the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--kernel-probe", default=None,
+                    help="only launch one workload and a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--roofline-probe", action="store_true",
+                    help="only measure the streaming-read and FP8 MFMA ceilings")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported "
               "(this path has no multi-GPU component)", file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        raise SystemExit("--steps must be >= 1 and --warmup >= 0")
 
     import torch
 
@@ -447,19 +590,24 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.kernel_probe:
-        kernel_probe(torch, dev)
+        kernel_probe(torch, dev, args.kernel_probe)
+        return
+    if args.roofline_probe:
+        print(json.dumps(roofline_ceilings(torch, dev)))
         return
 
     dec = decode_sweep(torch, dev, args.steps, args.warmup)
     value = dec["step_bytes"] / dec["step_s"] / 1e9
-    # dominant kernel: the largest share of the sweep's GEMM time
-    dom = max(dec["per_m"], key=lambda r: r["kernel_us"])
-    traffic = measured_traffic() if dom["M"] == PROBE_M else None
-    roofline = dict(bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(dom["gbs"] / HBM_PEAK_GBS, 4), traffic=traffic,
-                    kernel=f"GEMM launch at M={dom['M']}, K={K_DEC}, N={N_DEC}",
-                    bytes_per_launch=dom["bytes"], avg_us=dom["kernel_us"],
-                    traffic_source=os.path.relpath(TRAFFIC_PROFILE, ROOT) if traffic else None)
+    # the dominant op of the step: the largest time
+    dom = max(dec["per_m"], key=lambda r: r["op_us"])
+    traffic = profile_value(DECODE_COUNTERS, "traffic_bytes_per_op") if dom["M"] == PROBE_M else None
+    roofline = dict(bound="hbm", achieved=dom["op_gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(dom["op_gbs"] / HBM_PEAK_GBS, 4),
+                    traffic=int(traffic) if traffic else None,
+                    kernel=f"fp8_linear op at M={dom['M']}, K={K_DEC}, N={N_DEC}, bf16 in and out "
+                           f"(every launch it makes, as the step runs it)",
+                    bytes_per_launch=dom["op_bytes"], avg_us=dom["op_us"],
+                    traffic_source=f"profiles/{DECODE_COUNTERS}" if traffic else None)
     line = dict(metric=METRIC, value=round(value, 1), unit="GB/s", n_gpus=1, steps=dec["steps"],
                 warmup=args.warmup, ms_per_step=round(dec["step_s"] * 1e3, 4),
                 higher_is_better=True, scaling="weak", vs_baseline=None, dtype="fp8e4m3xfp8e4m3->f32",
@@ -469,9 +617,19 @@ def main():
                             "128x128 f32 block scales", out="bf16",
                             weight_copies_rotated=dec["copies"]),
                 roofline=roofline, sweep=dec["per_m"])
+    line["ceilings"] = roofline_ceilings(torch, dev)
     if not args.no_extras:
+        prefill = prefill_gemms(torch, dev, 20)
+        top = prefill[0]
+        busy = profile_value(PREFILL_COUNTERS, "mfma_busy_frac")
+        line["roofline_prefill"] = dict(
+            bound="mfma", achieved=top["gemm_tflops"], peak=FP8_PEAK_TFLOPS, unit="TFLOP/s",
+            frac=round(top["gemm_tflops"] / FP8_PEAK_TFLOPS, 4), traffic=None,
+            kernel=f"prefill GEMM launch of fp8_linear, M=8192, K={top['K']}, N={top['N']}, bf16 out",
+            flops_per_launch=2 * 8192 * top["K"] * top["N"], avg_us=top["gemm_us"],
+            mfma_busy_frac=busy, counters_source=f"profiles/{PREFILL_COUNTERS}" if busy else None)
         line["extras"] = dict(
-            prefill_gemm=prefill_gemms(torch, dev, 20),
+            prefill_gemm=prefill,
             moe_decode=moe_layer_bench(torch, dev, 256, False, 20),
             moe_prefill_zipf=moe_layer_bench(torch, dev, 16384, True, 10),
             rms_quantize=rms_quantize_bench(torch, dev),
