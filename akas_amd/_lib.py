@@ -46,6 +46,8 @@ SIGNATURES = {
                               _p]),
     "akas_expert_partial": (_i, [_p, _p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _i64, _i, _i,
                                  _i64, _i64, _i, _i, _i, _i, _p]),
+    "akas_expert_combine": (_i, [_p, _p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _p, _i, _p, _p, _i64,
+                                 _i, _i, _i64, _i64, _i, _i, _i, _p]),
     "akas_fp8_expert_swiglu": (_i, [_p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _p,
                                     _i64, _i, _i, _i64, _i64, _i, _i, _i, _i, _i, _p]),
     "akas_expert_swiglu": (_i, [_p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _i64, _i,

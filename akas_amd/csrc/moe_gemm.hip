@@ -36,6 +36,12 @@ struct ExpertArgs {
   void* out;
   void* out2;          // up partials (expert_pair_partial)
   float* out_scales;
+  // expert_combine: the routed_combine fold in the epilogue
+  const int32_t* ids;       // [r, top] expert ids (a rank is live when 0 <= id < E)
+  const float* cweights;    // [r, top] combine weights
+  const int32_t* active;    // [r] or null (every row active)
+  float* cout;              // [r, N] f32 combined rows
+  int32_t* arrivals;        // [r, N / BN] per (row, column block) arrival counts
   int r, top, E, N, K;
   int x_rows;    // rows addressable in x / as (gathered rows are clamped to it)
   int out_rows;  // rows addressable in out (r*top, or packed rows)
@@ -112,14 +118,110 @@ enum ExpertMode {
   kSwigluFp8 = 1,    // fp8_expert_swiglu: SwiGLU, per-128 FP8 codes + scales
   kSwiglu = 2,       // expert_swiglu: SwiGLU stored in OUT
   kPairPartial = 3,  // expert_pair_partial: gate -> out, up -> out2, f32 per part
+  kCombine = 4,      // expert_combine: kPartial's stores, then the rank-ordered fold
 };
+
+// Modes whose B tile holds gate and up rows.
+constexpr bool paired_mode(int mode) { return mode == kSwigluFp8 || mode == kSwiglu || mode == kPairPartial; }
+
+// Live ranks of row t: its ids inside [0, E) (the ranks quantized_routes
+// routes when the row is active).
+AKAS_DEV int live_ranks(const ExpertArgs& p, int t) {
+  int n = 0;
+  for (int k = 0; k < p.top; ++k) {
+    const int e = p.ids[(int64_t)t * p.top + k];
+    n += e >= 0 && e < p.E;
+  }
+  return n;
+}
+
+// expert_combine, rows no route reaches (inactive, or without a live rank):
+// their combined row is zero.  Row t belongs to workgroup t % gridDim.x, so
+// every workgroup of the grid, live or not, takes a share before its exit.
+template <int THREADS>
+AKAS_DEV void zero_unrouted_rows(const ExpertArgs& p) {
+  for (int t = blockIdx.x; t < p.r; t += gridDim.x) {
+    const bool routed = (!p.active || p.active[t] != 0) && live_ranks(p, t) > 0;  // uniform
+    if (routed) continue;
+    v4f* row = reinterpret_cast<v4f*>(p.cout + (int64_t)t * p.N);
+    for (int c = threadIdx.x; c < p.N / 4; c += THREADS) row[c] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+// expert_combine tail, after the workgroup has stored its contributions
+// (rows rows_dst[0..BM), columns n0 .. n0+BN) in CDT:
+//   * release fence, then one arrival per live row on the counter of its
+//     (token, column block); the arrival that completes the token's live
+//     ranks (every other rank's workgroup has stored and fenced before its
+//     own arrival) resets the counter to zero and takes the token;
+//   * if the workgroup took any token: acquire fence, then the taken tokens'
+//     combined columns: acc = 0, then acc = fma(contribution[token, rank],
+//     weight[token, rank], acc) over the live ranks in rank order --
+//     routed_combine's fold on the stored (rounded) contributions, so the
+//     result is the same bit for bit.
+// Exactly one arrival completes each counter, so no workgroup waits for
+// another and the counters are left zero for the next call.  On gfx950 the
+// device-scope release is an L2 write-back per workgroup (buffer_wbl2), the
+// price of handing the contributions across XCDs inside one launch.
+template <int BM, int BN, int THREADS, int CDT>
+AKAS_DEV void combine_tail(const ExpertArgs& p, const int* rows_dst, int* taken, int* ntaken,
+                           int nb, int n0) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  if (threadIdx.x == 0) *ntaken = 0;
+  __syncthreads();
+  const int blocks = p.N / BN;
+  for (int i = threadIdx.x; i < BM; i += THREADS) {
+    const int dst = rows_dst[i];
+    if (dst < 0) continue;
+    const int t = dst / p.top;
+    int32_t* counter = p.arrivals + (int64_t)t * blocks + nb;
+    const int before = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (before + 1 == live_ranks(p, t)) {
+      __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      taken[atomicAdd(ntaken, 1)] = t;  // LDS slot; the fold order is per token, not per slot
+    }
+  }
+  __syncthreads();
+  const int n = *ntaken;  // uniform
+  if (n == 0) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  constexpr int G = BN / 4;  // four columns per thread
+  for (int u = threadIdx.x; u < n * G; u += THREADS) {
+    const int t = taken[u / G];
+    const int col = n0 + 4 * (u % G);
+    const int64_t row = (int64_t)t * p.top;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < p.top; ++k) {
+      const int e = p.ids[row + k];
+      if (e < 0 || e >= p.E) continue;
+      const float w = p.cweights[row + k];
+      const int64_t at = (row + k) * p.N + col;
+      v4f v;
+      if constexpr (CDT == AKAS_DTYPE_F32) {
+        v = *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(p.out) + at);
+      } else {
+        const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p.out) + at);
+        if constexpr (CDT == AKAS_DTYPE_BF16) {
+          v = v4f{bf16_bits_to_f32(h.x & 0xFFFFu), bf16_bits_to_f32(h.x >> 16),
+                  bf16_bits_to_f32(h.y & 0xFFFFu), bf16_bits_to_f32(h.y >> 16)};
+        } else {
+          v = v4f{f16_bits_to_f32(h.x & 0xFFFFu), f16_bits_to_f32(h.x >> 16),
+                  f16_bits_to_f32(h.y & 0xFFFFu), f16_bits_to_f32(h.y >> 16)};
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(v[q], w, acc[q]);
+    }
+    *reinterpret_cast<v4f*>(p.cout + (int64_t)t * p.N + col) = acc;
+  }
+}
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int MODE, int OUT, int SDT>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(ExpertArgs p) {
   constexpr int THREADS = 64 * WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int MT = WM / 16, NT = WN / 16;
-  constexpr bool PAIRED = MODE != kPartial;
+  constexpr bool PAIRED = paired_mode(MODE);
   static_assert(!PAIRED || (BN == 256 && NT % 2 == 0), "paired tiles hold 128 gate + 128 up");
   static_assert(PAIRED || 128 % WN == 0, "a wave's columns must stay inside one scale block");
   using Plan = StagePlan<BM, BN, THREADS>;
@@ -128,14 +230,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
   // stage: 20.9 KB lets four workgroups share a CU instead of three, 38.6 ->
   // 36.6 us at 64 experts x 1536 -> 2048.  The paired gate/up kernel was
   // slower that way (86.8 -> 90.6 us) and keeps two.
-  constexpr int NSTAGE = (MODE == 0 && BM == 32) ? 1 : 2;
+  constexpr int NSTAGE = (!PAIRED && BM == 32) ? 1 : 2;
   __shared__ __attribute__((aligned(16))) uint8_t lds[NSTAGE * STAGE];
   __shared__ __attribute__((aligned(16))) float lds_as[NSTAGE][BM];
   __shared__ int rows_src[BM];
   __shared__ int rows_dst[BM];
   __shared__ float row_max[MODE == kSwigluFp8 ? WAVES_N : 1][MODE == kSwigluFp8 ? BM : 1];
+  __shared__ int taken[MODE == kCombine ? BM : 1];
+  __shared__ int ntaken;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if constexpr (MODE == kCombine) zero_unrouted_rows<THREADS>(p);
   // Tiles walked fastest, so the dead tiles past each column block's live
   // ones are spread evenly over the grid (no live-item enumeration needed).
   const int id = xcd_remap(blockIdx.x, p.max_tiles * p.tiles_n);
@@ -268,6 +373,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
                          acc.t[i][j][e4]);
         }
       }
+    if constexpr (MODE == kCombine) combine_tail<BM, BN, THREADS, OUT>(p, rows_dst, taken, &ntaken, nb, n0);
   } else if constexpr (MODE == kPairPartial) {
     const int64_t rstride = (int64_t)p.parts * p.N;
 #pragma unroll
@@ -372,14 +478,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
 // ---------------------------------------------------------------------------
 template <int MODE, int OUT, int SDT>
 __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) {
-  constexpr bool PAIRED = MODE != kPartial;
+  constexpr bool PAIRED = paired_mode(MODE);
   constexpr int BM = dma::BM;
   __shared__ int rows_src[BM];
   __shared__ int rows_dst[BM];
   __shared__ float row_max[MODE == kSwigluFp8 ? 2 : 1][MODE == kSwigluFp8 ? BM : 1];
+  __shared__ int taken[MODE == kCombine ? BM : 1];
+  __shared__ int ntaken;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if constexpr (MODE == kCombine) zero_unrouted_rows<dma::THREADS>(p);
   const int id = live_item(p.counts, p.E, BM, p.tiles_n, lane);
   if (id < 0) return;  // past the live items (uniform)
   const int nb = id % p.tiles_n, t = id / p.tiles_n;
@@ -449,6 +558,7 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
     dma::store_tile<OUT>(
         acc, p.out, wave, lane, [&](int r) { return rows_dst[a_row0 + r] >= 0; },
         [&](int r) { return (int64_t)rows_dst[a_row0 + r] * rstride + (int64_t)part * p.N + wcol; });
+    if constexpr (MODE == kCombine) combine_tail<BM, dma::BN, dma::THREADS, OUT>(p, rows_dst, taken, &ntaken, nb, n0);
   } else if constexpr (MODE == kPairPartial) {
     // Lane l holds, for m-tile i and column group c (0..3), gate in n-tile
     // 2c and up in n-tile 2c+1 of row a_row0 + 16i + l%16 at output columns
@@ -599,7 +709,7 @@ int64_t capacity_tiles(int64_t r, int64_t top, int64_t experts, int64_t bm) {
 template <int BM, int BN, int WMW, int WNW, int MODE, int OUT>
 static void launch_expert(ExpertArgs a, hipStream_t s) {
   a.max_tiles = (int)capacity_tiles(a.r, a.top, a.E, BM);
-  a.tiles_n = MODE != kPartial ? a.N / (BN / 2) : a.N / BN;
+  a.tiles_n = paired_mode(MODE) ? a.N / (BN / 2) : a.N / BN;
   dim3 grid((unsigned)(a.max_tiles * a.tiles_n), (unsigned)a.parts);
   if (a.ws_dtype == AKAS_DTYPE_F32)
     expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_F32><<<grid, 64 * WMW * WNW, 0, s>>>(a);
@@ -610,7 +720,7 @@ static void launch_expert(ExpertArgs a, hipStream_t s) {
 template <int MODE, int OUT>
 static void launch_expert_dma(ExpertArgs a, hipStream_t s) {
   a.max_tiles = (int)capacity_tiles(a.r, a.top, a.E, dma::BM);
-  a.tiles_n = MODE != kPartial ? a.N / (dma::BN / 2) : a.N / dma::BN;
+  a.tiles_n = paired_mode(MODE) ? a.N / (dma::BN / 2) : a.N / dma::BN;
   dim3 grid((unsigned)(a.max_tiles * a.tiles_n), (unsigned)a.parts);
   if (a.ws_dtype == AKAS_DTYPE_F32)
     expert_dma_kernel<MODE, OUT, AKAS_DTYPE_F32><<<grid, dma::THREADS, 0, s>>>(a);
@@ -626,15 +736,15 @@ static bool expert_dma_fits(const ExpertArgs& a, int64_t mean, int64_t n_mult) {
 
 // Row tile by the mean rows per expert: 32-row tiles for decode-like batches,
 // 128-row tiles in between, DMA-fed 256-row tiles for prefill batches.
-template <int OUT>
+template <int OUT, int MODE = kPartial>
 static void launch_partial(const ExpertArgs& a, hipStream_t s) {
   const int64_t mean = (int64_t)a.r * a.top / a.E;
   if (mean <= 48)
-    launch_expert<32, 128, 1, 4, 0, OUT>(a, s);
+    launch_expert<32, 128, 1, 4, MODE, OUT>(a, s);
   else if (expert_dma_fits(a, mean, dma::BN))
-    launch_expert_dma<0, OUT>(a, s);
+    launch_expert_dma<MODE, OUT>(a, s);
   else
-    launch_expert<128, 128, 2, 2, 0, OUT>(a, s);
+    launch_expert<128, 128, 2, 2, MODE, OUT>(a, s);
 }
 
 // The paired kernels (modes 1-3), row tile by the mean rows per expert as
@@ -713,6 +823,46 @@ extern "C" int akas_expert_partial(const uint8_t* x, const float* activation_sca
     case AKAS_DTYPE_F32: launch_partial<AKAS_DTYPE_F32>(a, s); break;
     case AKAS_DTYPE_BF16: launch_partial<AKAS_DTYPE_BF16>(a, s); break;
     default: launch_partial<AKAS_DTYPE_F16>(a, s);
+  }
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_expert_combine(const uint8_t* x, const float* activation_scales,
+                                   const uint8_t* w, const void* w_scales, int scale_dtype,
+                                   const int32_t* counts, const int32_t* routes,
+                                   const int32_t* expert_offsets, const int32_t* ids,
+                                   const float* weights, const int32_t* active,
+                                   void* contributions, int contribution_dtype, float* out,
+                                   int32_t* arrivals, int64_t r, int top, int experts, int64_t o,
+                                   int64_t k, int routed_input, int max_block_m, int packed_input,
+                                   void* stream) {
+  const int64_t x_rows = packed_input ? capacity_tiles(r, top, experts, max_block_m) * max_block_m
+                                      : (routed_input ? r * top : r);
+  int st = check_common(r, top, experts, o, k, max_block_m, packed_input, x_rows);
+  if (st != AKAS_OK) return st;
+  if (!float_dtype(contribution_dtype) || !scale_dtype_ok(scale_dtype)) return AKAS_ERR_DTYPE;
+  if (r == 0) return AKAS_OK;
+  if (!x || !activation_scales || !w || !w_scales || !counts || !routes || !ids || !weights ||
+      !contributions || !out || !arrivals)
+    return AKAS_ERR_NULL;
+  if (packed_input && !expert_offsets) return AKAS_ERR_NULL;
+  if (reinterpret_cast<uintptr_t>(contributions) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
+    return AKAS_ERR_GEOMETRY;
+  ExpertArgs a{};
+  a.x = x; a.as = activation_scales; a.w = w; a.ws = w_scales;
+  a.counts = counts; a.routes = routes; a.offsets = expert_offsets; a.out = contributions;
+  a.ids = ids; a.cweights = weights; a.active = active; a.cout = out; a.arrivals = arrivals;
+  a.r = (int)r; a.top = top; a.E = experts; a.N = (int)o; a.K = (int)k;
+  a.routed = routed_input; a.packed_in = packed_input; a.packed_out = 0;
+  a.x_rows = (int)x_rows; a.out_rows = (int)(r * top);
+  a.parts = 1; a.kb_per_part = (int)(k / kBlock);
+  a.ws_dtype = scale_dtype;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (contribution_dtype) {
+    case AKAS_DTYPE_F32: launch_partial<AKAS_DTYPE_F32, kCombine>(a, s); break;
+    case AKAS_DTYPE_BF16: launch_partial<AKAS_DTYPE_BF16, kCombine>(a, s); break;
+    default: launch_partial<AKAS_DTYPE_F16, kCombine>(a, s);
   }
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;

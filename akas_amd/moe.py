@@ -8,7 +8,8 @@ src/akas/ops/moe/definition.py:442-540, 677-793, 951-1053):
     router + quantize(x) (one launch up to 64 experts and top 8)
       -> quantized_routes [-> expert_pack] -> fp8_expert_swiglu (or expert_partial x2 ->
       swiglu_experts -> quantize) -> expert_partial(down, routed_input)
-      -> routed_combine
+      -> routed_combine (or expert_combine: the down projection with
+      routed_combine folded into its epilogue)
 
 The reference program also builds ``expert_tile_map`` between the routes and
 the products, because its grouped kernels read their (expert, row tile) from
@@ -88,14 +89,19 @@ class SharedExpert:
 
 def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed, max_block_m,
                           product_dtype, activation_dtype, contribution_dtype, quantized=None,
-                          partitions=1):
+                          partitions=1, combine_weights=None):
     """Routes, FP8 activations and the grouped expert products:
     ``[T, top, H]`` contributions in ``contribution_dtype``.  ``quantized``:
     x's codes and scales when the caller made them already.  ``partitions``
     > 1 splits every expert product over K as the reference's partitions
     policy does (src/akas/ops/moe/definition.py:796-948): gate/up through
     expert_pair_partial -> swiglu_experts -> quantize, the down projection
-    through expert_partial(partitions) -> expert_merge."""
+    through expert_partial(partitions) -> expert_merge.
+
+    Returns ``(contributions, counts, routes, combined)``: with
+    ``combine_weights`` (and ``partitions`` 1) the down projection is
+    ``expert_combine``, which also folds the weighted combine, and
+    ``combined`` is its f32 ``[T, H]``; otherwise ``combined`` is None."""
     rows, hidden = x.shape
     experts = weights.experts
     counts, routes = ops.quantized_routes(ids, active, experts=experts)
@@ -120,7 +126,7 @@ def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed,
         partial = ops.expert_partial(act, act_scales, weights.w2, weights.s2, counts, routes,
                                      tile_experts, tile_rows, routed_input=True,
                                      partitions=partitions, **common)
-        return ops.expert_merge(partial, output_dtype=contribution_dtype), counts, routes
+        return ops.expert_merge(partial, output_dtype=contribution_dtype), counts, routes, None
     if fused_swiglu:
         act_rows = ((ops.tile_capacity(rows, top, experts, max_block_m) * max_block_m,) if packed
                     else (rows, top))
@@ -139,26 +145,39 @@ def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed,
                                 tile_experts, tile_rows, output_dtype=product_dtype, **common)
         activated = ops.swiglu_experts(gate, up, output_dtype=activation_dtype)
         act, act_scales = ops.quantize(activated, top=top)
+    contributions = torch.empty((rows, top, hidden), dtype=ops._torch_dtype(contribution_dtype),
+                                device=x.device)
+    if combine_weights is not None:
+        combined, contributions = ops.expert_combine(
+            act, act_scales, weights.w2, weights.s2, counts, routes, ids, combine_weights,
+            active, offsets, routed_input=not packed, packed_input=packed,
+            contribution_dtype=contribution_dtype, contributions=contributions, **common)
+        return contributions, counts, routes, combined
     contributions = ops.expert_partial(
         act, act_scales, weights.w2, weights.s2, counts, routes, tile_experts, tile_rows,
         offsets, routed_input=not packed, packed_input=packed, output_dtype=contribution_dtype,
-        out=torch.empty((rows, top, hidden), dtype=ops._torch_dtype(contribution_dtype),
-                        device=x.device),
-        **common)
-    return contributions, counts, routes
+        out=contributions, **common)
+    return contributions, counts, routes, None
 
 
 def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
                router="biased_softmax_router", scale=1.0, normalize=True, fused_swiglu=True,
                packed=False, max_block_m=64, product_dtype=torch.float32,
                activation_dtype=torch.float32, contribution_dtype=torch.float32,
-               partitions=1, partition_maximum_rows=None, return_routing=False):
+               partitions=1, partition_maximum_rows=None, fused_combine=False,
+               return_routing=False):
     """One routed MoE feed-forward: ``x [T, H]`` (f32/f16/bf16) -> f32 ``[T, H]``.
 
     ``partitions`` > 1 applies the reference's K-partition policy to batches
     of at most ``partition_maximum_rows`` rows (all batches when None), as
     its one-row decode seed does (``partitions: 2, partition_maximum_rows:
-    1``, src/akas/ops/moe/definition.py:637-652).
+    1``, src/akas/ops/moe/definition.py:637-652).  ``fused_combine`` folds
+    ``routed_combine`` into the down projection's epilogue
+    (``expert_combine``, the same result bit for bit).  It is off by default:
+    handing every workgroup's contributions to another XCD inside the launch
+    costs a device-scope release (an L2 write-back) per workgroup, which on
+    MI355X outweighs the combine launch it saves.  With partitions the down
+    projection keeps expert_partial -> expert_merge -> routed_combine.
     """
     if router not in ("biased_router", "biased_softmax_router"):
         raise ValueError("unknown routed expert scoring")
@@ -183,12 +202,14 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
                                              normalize=normalize)
     else:
         ids, probability = ops.biased_softmax_router(logits, bias, top=top, scale=scale)
-    contributions, counts, routes = _expert_contributions(
+    contributions, counts, routes, out = _expert_contributions(
         x, ids, active, weights, top=top, fused_swiglu=fused_swiglu, packed=packed,
         max_block_m=max_block_m, product_dtype=product_dtype,
         activation_dtype=activation_dtype, contribution_dtype=contribution_dtype,
-        quantized=quantized, partitions=partitions)
-    out = ops.routed_combine(contributions, probability, active)
+        quantized=quantized, partitions=partitions,
+        combine_weights=probability if fused_combine and partitions == 1 else None)
+    if out is None:
+        out = ops.routed_combine(contributions, probability, active)
     if return_routing:
         return out, dict(ids=ids, weights=probability, counts=counts, routes=routes)
     return out
@@ -251,7 +272,7 @@ def shared_expert_moe(x, logits, shared_gate, weights: ExpertWeights, shared: Sh
     if routed_kinds == "groups":
         contributions = _group_contributions(x, ids, weights, top=top)
     elif routed_kinds == "routes":
-        contributions, _, _ = _expert_contributions(
+        contributions, _, _, _ = _expert_contributions(
             x, ids, _all_active(rows, x.device), weights, top=top, fused_swiglu=fused_swiglu,
             packed=packed, max_block_m=max_block_m, product_dtype=torch.float32,
             activation_dtype=torch.float32, contribution_dtype=contribution_dtype)

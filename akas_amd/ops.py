@@ -488,6 +488,77 @@ def expert_partial(x, activation_scales, w, scales, counts, routes, tile_experts
     return out
 
 
+_ARRIVALS = {}  # (device index, stream handle) -> expert_combine arrival counters
+
+
+def combine_arrivals(r, o, device, stream=None):
+    """Arrival counters of :func:`expert_combine`, one zeroed buffer per device
+    and stream (every call leaves its counters zero again, so calls ordered
+    on one stream share it).  An outgrown buffer is retired, never freed."""
+    need = r * (o // BLOCK)
+    device = torch.device(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if stream is None:
+        stream = torch.cuda.current_stream(index)
+    key = (index, stream.cuda_stream)
+    buf = _ARRIVALS.get(key)
+    if buf is None or buf.numel() < need:
+        if buf is not None:
+            _RETIRED.append(buf)
+        buf = torch.zeros(max(need, 1 << 16), dtype=torch.int32, device=torch.device("cuda", index))
+        _ARRIVALS[key] = buf
+    return buf
+
+
+def expert_combine(x, activation_scales, w, scales, counts, routes, ids, weights, active=None,
+                   expert_offsets=None, *, r, top, routed_input=False, packed_input=False,
+                   contribution_dtype=torch.float32, max_block_m=64, contributions=None,
+                   out=None, arrivals=None):
+    """The down projection with ``routed_combine`` folded into its epilogue:
+    ``expert_partial`` (``partitions`` 1, ``contribution_dtype``) and
+    ``routed_combine`` in one launch, bit-identical to that pair
+    (src/akas/ops/moe/cuda.py:541-1354 scatter :956-966;
+    src/akas/ops/moe/kernel.py:206-267).
+
+    Returns ``(out, contributions)``: f32 ``[r, o]`` and the ``[r, top, o]``
+    contributions in ``contribution_dtype``.  ``counts``/``routes`` must be
+    ``quantized_routes(ids, active)``; a rank is folded when its id is in
+    ``[0, experts)``.
+    """
+    _need(x, "x", torch.uint8)
+    _need(w, "w", torch.uint8)
+    experts, o, k = w.shape
+    _need(scales, "scales", _SCALES, (experts, (o + BLOCK - 1) // BLOCK, k // BLOCK))
+    _need(counts, "counts", torch.int32, (experts,))
+    _need(routes, "routes", torch.int32, (experts, r))
+    _need(ids, "ids", torch.int32, (r, top))
+    _need(weights, "weights", torch.float32, (r, top))
+    if active is not None:
+        _need(active, "active", torch.int32, (r,))
+    if x.shape[-1] != k:
+        raise ValueError("activation depth differs from the expert weights")
+    _need(activation_scales, "activation_scales", torch.float32, (*x.shape[:-1], k // BLOCK))
+    if packed_input and expert_offsets is None:
+        raise ValueError("packed expert input requires expert_offsets")
+    cdt = _torch_dtype(contribution_dtype)
+    if contributions is None:
+        contributions = torch.empty((r, top, o), dtype=cdt, device=x.device)
+    _need(contributions, "contributions", cdt, (r, top, o))
+    out = _out(out, "out", (r, o), torch.float32, x)
+    if arrivals is None:
+        arrivals = combine_arrivals(r, o, x.device)
+    _need(arrivals, "arrivals", torch.int32)
+    if arrivals.numel() < r * (o // BLOCK):
+        raise ValueError("arrivals holds fewer than r * o / 128 counters")
+    check(_lib.load().akas_expert_combine(
+        _ptr(x), _ptr(activation_scales), _ptr(w), _ptr(scales), _dt(scales.dtype), _ptr(counts),
+        _ptr(routes), _ptr(expert_offsets), _ptr(ids), _ptr(weights), _ptr(active),
+        _ptr(contributions), _dt(cdt), _ptr(out), _ptr(arrivals), r, top, experts, o, k,
+        int(bool(routed_input)), max_block_m, int(bool(packed_input)), _stream()),
+        "expert_combine")
+    return out, contributions
+
+
 def fp8_experts_workspace(r, top, experts, k, routed_input, device):
     """Workspace of :func:`fp8_experts` (quantized input and the per-expert
     route tables built from the group tables)."""

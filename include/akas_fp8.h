@@ -309,6 +309,39 @@ int akas_expert_partial(const uint8_t* x, const float* activation_scales, const 
                         void* stream);
 
 /*
+ * expert_combine(r, top, experts, o, k, routed_input[, max_block_m,
+ * contribution_dtype, packed_input]): x, activation_scales, w, scales,
+ * counts, routes[, expert_offsets], ids, weights[, active] -> contributions,
+ * out.
+ * The down projection with routed_combine folded into its epilogue: the
+ * expert_partial product scattered to (row, rank) (src/akas/ops/moe/
+ * cuda.py:541-1354, the scatter at :956-966) followed by routed_combine
+ * (src/akas/ops/moe/kernel.py:206-267) in one launch, bit-identical to
+ * expert_partial(partitions = 1, contribution_dtype) -> routed_combine.
+ *   contributions: [r, top, o] in contribution_dtype (f32/f16/bf16), written
+ *     for every routed (row, rank) as expert_partial writes them;
+ *   out: f32 [r, o]; out[b, c] = fma-fold over the live ranks of row b in
+ *     rank order of contributions[b, rank, c] * weights[b, rank] (starting
+ *     from 0); rows with active == 0 (active may be null: every row active)
+ *     or with no live rank are zero.  A rank is live when
+ *     0 <= ids[b, rank] < experts -- exactly the ranks quantized_routes
+ *     routes, so counts/routes must be quantized_routes(ids, active).
+ *   arrivals: int32 [r, o / 128]; zero before the first call, and every call
+ *     leaves it zero.  Calls that share one arrivals buffer must not
+ *     overlap (use one buffer per stream).
+ * contributions and out 16-byte aligned; o % 128 == 0, k % 128 == 0.
+ * The workgroup whose stored tile completes a row's live ranks for a column
+ * block folds that row's block; no workgroup waits for another.
+ */
+int akas_expert_combine(const uint8_t* x, const float* activation_scales, const uint8_t* w,
+                        const void* w_scales, int scale_dtype, const int32_t* counts,
+                        const int32_t* routes, const int32_t* expert_offsets, const int32_t* ids,
+                        const float* weights, const int32_t* active, void* contributions,
+                        int contribution_dtype, float* out, int32_t* arrivals, int64_t r,
+                        int top, int experts, int64_t o, int64_t k, int routed_input,
+                        int max_block_m, int packed_input, void* stream);
+
+/*
  * fp8_experts(r, experts, top, o, k, routed_input): x, w, scales, experts,
  * routes -> out (the block-fp8 decode variant's expert products).
  * Replaces src/akas/ops/moe/cuda.py:439-531.  x f32/f16/bf16 [r, k] (or

@@ -492,6 +492,25 @@ def routed_combine(experts, weights, active):
     return out
 
 
+def expert_combine(x, activation_scales, w, scales, counts, routes, ids, weights, active, top,
+                   routed_input=False, contribution_dtype="float32"):
+    """The down projection with the weighted combine folded in: the
+    ``expert_partial`` contributions (``partitions`` 1, rounded to
+    ``contribution_dtype``) and ``routed_combine`` over each row's live ranks
+    (ids inside ``[0, E)``, the ranks ``quantized_routes`` routes); rows
+    without a live rank, and inactive rows, are 0.  Composes
+    ``expert_partial`` (``src/akas/ops/moe/cuda.py:541-1354``, scatter
+    ``:956-966``) and ``routed_combine`` (``src/akas/ops/moe/kernel.py:206-267``).
+    Returns ``(out float32 [r, o], contributions [r, top, o])``."""
+    ids = np.asarray(ids, np.int64)
+    E = w.shape[0]
+    contributions = expert_partial(x, activation_scales, w, scales, counts, routes, top,
+                                   routed_input=routed_input, output_dtype=contribution_dtype)
+    live = (ids >= 0) & (ids < E)
+    out = routed_combine(np.where(live[:, :, None], contributions, 0.0), weights, active)
+    return out, contributions
+
+
 def moe_combine(experts, weights, shared, gate):
     """Weighted top-k combine plus a sigmoid-gated shared expert:
     ``sum_rank bf16(e) * w + bf16(shared) / (1 + exp(-bf16(gate)))``.

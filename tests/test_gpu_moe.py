@@ -727,6 +727,133 @@ def test_routed_combine(dev, in_dtype, top, c):
     np.testing.assert_allclose(_np(out), omoe.routed_combine(e, w, active), rtol=1e-5, atol=1e-6)
 
 
+COMBINE_CASES = [
+    # rows, top, experts, o, k, routed, packed, max_block_m, contribution dtype
+    (256, 4, 64, 512, 256, True, False, 64, "bfloat16"),   # 32-row tiles (decode)
+    (256, 4, 64, 512, 256, True, False, 64, "float32"),
+    (1, 4, 64, 256, 256, True, False, 64, "float32"),
+    (700, 4, 16, 384, 256, True, False, 64, "float16"),    # 128-row tiles
+    (1500, 2, 6, 512, 384, True, False, 64, "bfloat16"),   # 256-row DMA tiles
+    (1024, 4, 8, 512, 256, False, True, 128, "bfloat16"),  # packed input, DMA tiles
+    (1024, 4, 8, 512, 256, True, True, 128, "float32"),    # packed routed input
+    (600, 3, 5, 256, 256, False, True, 128, "float32")]
+
+
+def _combine_inputs(dev, rng, rows, top, experts, o, k, routed, packed, maxm):
+    import torch
+    from akas_amd import ops
+
+    ids, active, counts, routes, x, xs, w, ws = _expert_case(rng, rows, top, experts, o, k, routed,
+                                                             exact=False, mult=3)
+    cw = rng.uniform(0, 1, (rows, top)).astype(np.float32)
+    d = dict(ids=_t(ids, dev), active=_t(active, dev), counts=_t(counts, dev),
+             routes=_t(routes, dev), w=_t(w, dev), ws=_t(ws, dev, torch.bfloat16), cw=_t(cw, dev),
+             offsets=None, x=_t(x, dev), xs=_t(xs, dev))
+    if packed:
+        d["x"], d["xs"], d["offsets"] = ops.expert_pack(d["x"], d["xs"], d["counts"], d["routes"],
+                                                        None, None, top=top, max_block_m=maxm,
+                                                        routed_input=routed)
+    return d, (ids, active, counts, routes, x, xs, w, ws, cw)
+
+
+def _routed_mask(ids, active, experts):
+    return (active[:, None] != 0) & (ids >= 0) & (ids < experts)
+
+
+@pytest.mark.parametrize("rows,top,experts,o,k,routed,packed,maxm,cdt", COMBINE_CASES)
+def test_expert_combine_matches_partial_then_combine(dev, rows, top, experts, o, k, routed, packed,
+                                                     maxm, cdt):
+    """expert_combine (down projection with the combine folded into its
+    epilogue) against expert_partial -> routed_combine on the device: the
+    combined rows and every routed contribution bit for bit, on every tile
+    shape (32-row, 128-row, DMA-fed 256-row; packed input); the arrival
+    counters are zero again after each of two calls."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(53 + rows)
+    d, host = _combine_inputs(dev, rng, rows, top, experts, o, k, routed, packed, maxm)
+    ct = getattr(torch, cdt)
+    common = dict(r=rows, top=top, max_block_m=maxm, routed_input=routed and not packed,
+                  packed_input=packed)
+    ref_c = ops.expert_partial(d["x"], d["xs"], d["w"], d["ws"], d["counts"], d["routes"], None,
+                               None, d["offsets"], output_dtype=ct, **common)
+    ref = ops.routed_combine(ref_c, d["cw"], d["active"])
+    arrivals = torch.zeros(rows * (o // 128), dtype=torch.int32, device=dev)
+    for _ in range(2):
+        out, contrib = ops.expert_combine(d["x"], d["xs"], d["w"], d["ws"], d["counts"], d["routes"],
+                                          d["ids"], d["cw"], d["active"], d["offsets"],
+                                          contribution_dtype=ct, arrivals=arrivals, **common)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        mask = torch.from_numpy(_routed_mask(host[0], host[1], experts)).to(dev)
+        assert torch.equal(contrib[mask], ref_c[mask])
+        assert not arrivals.any()
+
+
+def test_expert_combine_dead_ranks_and_inactive_rows(dev):
+    """Rows whose ids leave [0, experts) keep only their live ranks, a row
+    with no live rank and an inactive row are zero; exact products, so the
+    contributions equal the oracle's and the fold is within an f32 rounding
+    per rank of its float32 loop."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(59)
+    rows, top, experts, o, k = 300, 4, 16, 256, 256
+    ids, active = pattern_routes(rows, top, experts, 3)
+    ids[3, 2] = 99
+    ids[10, :] = -1
+    active[20] = 0
+    x = exact_codes(rng, (rows, k))
+    xs = (2.0 ** rng.integers(-4, 1, (rows, k // 128))).astype(np.float32)
+    w = exact_codes(rng, (experts, o, k))
+    ws = (2.0 ** rng.integers(-4, 1, (experts, o // 128, k // 128))).astype(np.float32)
+    cw = rng.uniform(0, 1, (rows, top)).astype(np.float32)
+    counts, routes = ops.quantized_routes(_t(ids, dev), _t(active, dev), experts=experts)
+    out, contrib = ops.expert_combine(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev), counts,
+                                      routes, _t(ids, dev), _t(cw, dev), _t(active, dev), r=rows,
+                                      top=top, contribution_dtype=torch.float32)
+    hc, hr = omoe.quantized_routes(ids, active, experts)
+    exp, exp_c = omoe.expert_combine(x, xs, w, ws, hc, hr, ids, cw, active, top)
+    mask = _routed_mask(ids, active, experts)
+    np.testing.assert_array_equal(_np(contrib)[mask], exp_c[mask])
+    got = _np(out)
+    # per rank the device rounds once (fma) and the oracle twice: at most
+    # 2 * top half-ulps of the running magnitude sum|c * w|
+    live = np.where(mask[:, :, None], np.abs(exp_c.astype(np.float64)), 0.0)
+    bound = 2 * top * 2.0 ** -24 * (live * cw[:, :, None]).sum(1)
+    assert (np.abs(got.astype(np.float64) - exp) <= bound).all()
+    assert not got[10].any() and not got[20].any()
+
+
+def test_expert_combine_graph_replays(dev):
+    """expert_combine captured in a HIP graph: three replays, each after eager
+    calls that change the output buffer, equal the eager result."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(61)
+    rows, top, experts, o, k = 256, 4, 64, 512, 256
+    d, _ = _combine_inputs(dev, rng, rows, top, experts, o, k, True, False, 64)
+    args = (d["x"], d["xs"], d["w"], d["ws"], d["counts"], d["routes"], d["ids"], d["cw"],
+            d["active"])
+    kw = dict(r=rows, top=top, routed_input=True, contribution_dtype=torch.bfloat16)
+    eager, _ = ops.expert_combine(*args, **kw)
+    out = torch.empty_like(eager)
+    ops.expert_combine(*args, out=out, **kw)  # warm the stream's arrival buffer
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.expert_combine(*args, out=out, **kw)
+    for _ in range(3):
+        out.fill_(7.0)
+        ops.expert_combine(*args, **kw)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
 # ---------------------------------------------------------------------------
 # the whole layer
 # ---------------------------------------------------------------------------
@@ -866,6 +993,11 @@ def test_routed_moe_layer_lfm2_dims(dev, lfm2_bank, rows, packed, zipf):
     exp, _, _ = omoe.moe_layer(x, logits, np.zeros(E, np.float32), *host, 4,
                                activation_dtype="bfloat16", contribution_dtype="bfloat16")
     assert rel_fro(_np(out), exp) < 1e-2
+    # the combine folded into the down epilogue equals the separate combine
+    fused = moe.routed_moe(_t(x, dev, bf), _t(logits, dev), None, wts, top=4, packed=packed,
+                           max_block_m=128 if packed else 64, product_dtype=bf,
+                           activation_dtype=bf, contribution_dtype=bf, fused_combine=True)
+    assert torch.equal(out, fused)
 
 
 def test_routed_moe_layer_zipf_prefill_full_size(dev, lfm2_bank):
@@ -1106,7 +1238,8 @@ def test_shared_expert_moe_block_graph_replays(dev):
 
 
 @pytest.mark.parametrize("packed", [False, True])
-def test_routed_moe_layer_graph_replays(dev, packed):
+@pytest.mark.parametrize("fused_combine", [False, True])
+def test_routed_moe_layer_graph_replays(dev, packed, fused_combine):
     """The routed block captured in a HIP graph: every replay (with eager work
     and synchronizations between them) equals the eager result."""
     import torch
@@ -1120,7 +1253,7 @@ def test_routed_moe_layer_graph_replays(dev, packed):
     wts = moe.ExpertWeights(*(_t(a, dev) for n in ("w1", "w3", "w2") for a in bank[n]))
     x = _t(bf16_normal(rng, (rows, H)), dev, torch.bfloat16)
     logits = _t(rng.normal(0, 1, (rows, E)).astype(np.float32), dev)
-    kw = dict(top=top, packed=packed, max_block_m=128 if packed else 64)
+    kw = dict(top=top, packed=packed, max_block_m=128 if packed else 64, fused_combine=fused_combine)
     eager = moe.routed_moe(x, logits, None, wts, **kw).clone()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())

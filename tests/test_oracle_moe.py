@@ -472,6 +472,43 @@ def test_routed_combine_loop():
             assert out[t, col] == (acc if active[t] else 0)
 
 
+@pytest.mark.parametrize("routed", [False, True])
+def test_expert_combine_exact(routed):
+    """expert_combine against exact products and a per-rank float32 fold:
+    an out-of-range id drops its rank (quantized_routes routes no entry for
+    it), a row whose ids are all out of range and an inactive row are zero."""
+    rng = np.random.default_rng(43)
+    rows, top, experts, o, k = 24, 3, 5, 256, 256
+    ids, active = _pattern(rows, top, experts, 1)
+    ids[2, 1] = experts      # one dead rank
+    ids[5, :] = -1           # no live rank
+    active[7] = 0
+    counts, routes = omoe.quantized_routes(ids, active, experts)
+    shape = (rows, top, k) if routed else (rows, k)
+    x = exact_codes(rng, shape)
+    xs = (2.0 ** rng.integers(-4, 2, (*shape[:-1], k // 128))).astype(np.float32)
+    w = exact_codes(rng, (experts, o, k))
+    ws = (2.0 ** rng.integers(-4, 2, (experts, o // 128, k // 128))).astype(np.float32)
+    cw = rng.uniform(0, 1, (rows, top)).astype(np.float32)
+    out, contributions = omoe.expert_combine(x, xs, w, ws, counts, routes, ids, cw, active, top,
+                                             routed_input=routed, contribution_dtype="bfloat16")
+    for t in range(rows):
+        for col in range(0, o, 37):
+            acc = np.float32(0)
+            for rank in range(top):
+                e = int(ids[t, rank])
+                if not (active[t] and 0 <= e < experts):
+                    continue
+                src = x[t, rank] if routed else x[t]
+                srcs = xs[t, rank] if routed else xs[t]
+                prod = _int_products(src[None], srcs[None], w[e][col:col + 1], ws[e][col // 128:col // 128 + 1])
+                c = ofp8.bf16_round(np.float32(prod[0, 0]))
+                assert contributions[t, rank, col] == c
+                acc = np.float32(acc + np.float32(c * cw[t, rank]))
+            assert out[t, col] == acc
+    assert not out[5].any() and not out[7].any()
+
+
 def test_moe_layer_against_per_token_loop():
     """The composed layer equals a per-token loop over its selected experts
     built from the pinned pieces (quantize, dequantize, SwiGLU, combine)."""
