@@ -25,6 +25,7 @@ config).
     python bench.py --kernel-probe {decode,prefill,moe_decode,moe_prefill,copy}
                                   # launches for rocprofv3 --pmc passes
     python bench.py --roofline-probe   # the measured ceilings alone
+    python bench.py --handoff-probe    # fences and atomics between workgroups
 """
 
 import argparse
@@ -563,6 +564,37 @@ def roofline_ceilings(torch, dev):
                 source="akas_amd/csrc/probe/roofline.hip")
 
 
+HANDOFF_MODES = {"plain": 0, "atomic": 4, "release+atomic": 5, "atomic+acquire": 6,
+                 "release+atomic+acquire": 7, "release+atomic+acquire+read": 15}
+
+
+def handoff_probe(torch, dev):
+    """Cost per launch of a hand-off between workgroups inside one launch
+    (device-scope release / acquire fences and one shared-counter atomic per
+    workgroup), graph-timed over 20 launches, by workgroup count and bytes
+    written per workgroup."""
+    import ctypes
+
+    from akas_amd import build
+
+    lib = ctypes.CDLL(build.PROBE_LIBRARY)
+    lib.akas_probe_handoff.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_void_p]
+    data = torch.zeros(1024 * 16384, dtype=torch.int32, device=dev)
+    counter = torch.zeros(257, dtype=torch.int32, device=dev)
+    rows = []
+    for blocks in (8, 64, 256, 1024):
+        for words in (1024, 16384):
+            row = dict(workgroups=blocks, bytes_per_workgroup=4 * words)
+            for name, mode in HANDOFF_MODES.items():
+                us = time_kernel_graph(torch, lambda i: lib.akas_probe_handoff(
+                    data.data_ptr(), counter.data_ptr(), blocks, words, mode,
+                    torch.cuda.current_stream().cuda_stream), 20) * 1e3
+                row[name] = round(us, 2)
+            rows.append(row)
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -574,6 +606,8 @@ def main():
                     help="only launch one workload and a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--roofline-probe", action="store_true",
                     help="only measure the streaming-read and FP8 MFMA ceilings")
+    ap.add_argument("--handoff-probe", action="store_true",
+                    help="only measure the cost of fences and atomics between workgroups")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported "
@@ -594,6 +628,10 @@ def main():
         return
     if args.roofline_probe:
         print(json.dumps(roofline_ceilings(torch, dev)))
+        return
+    if args.handoff_probe:
+        for row in handoff_probe(torch, dev):
+            print(json.dumps(row))
         return
 
     dec = decode_sweep(torch, dev, args.steps, args.warmup)
