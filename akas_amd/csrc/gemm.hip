@@ -622,8 +622,16 @@ constexpr size_t wide_lds_bytes(int kbp) {
 // while it is staged -- 16 lanes per 1x128 group, the same quantize8 as the
 // standalone quantizer, so the codes are identical -- which saves the
 // quantizer's launch and its codes' round trip for decode-sized batches.
-template <int MT, int NTW, int KS, int OUT, int SDT, int QX = 0>
+//
+// CW: output columns per workgroup (NTW 16-column tiles; the last tile may
+// hold fewer than 16 valid columns -- its other lanes re-read the last valid
+// weight row and store nothing), so that N / CW workgroups can match the CU
+// count: at N = 6144, 24 columns give 256 workgroups where 32 give 192.
+// A 24-column workgroup loads its weight scales per lane (its tiles can
+// straddle a 128-column scale block).
+template <int MT, int NTW, int KS, int OUT, int SDT, int QX = 0, int CW = 16 * NTW>
 __global__ __launch_bounds__(64 * NTW * KS) void dense_wide_kernel(DenseArgs p) {
+  static_assert(CW > 16 * (NTW - 1) && CW <= 16 * NTW, "columns per workgroup fill NTW tiles");
   constexpr int THREADS = 64 * NTW * KS;
   constexpr int ROWS = 16 * MT;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -634,10 +642,14 @@ __global__ __launch_bounds__(64 * NTW * KS) void dense_wide_kernel(DenseArgs p) 
   float* lds_s = reinterpret_cast<float*>(smem + (size_t)kbp * ROWS * 128);  // [kbp][ROWS]
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nt = wave % NTW, ks = wave / NTW;
-  const int n0 = blockIdx.x * (16 * NTW) + nt * 16;
+  const int n0 = blockIdx.x * CW + nt * 16;
+  const int valid = min(16, CW - nt * 16);  // valid columns of this tile
   const int g = lane >> 4, r16 = lane & 15;
-  const uint8_t* wrow = p.w + (int64_t)(n0 + r16) * p.K + g * 32;
-  const int64_t ws_base = (int64_t)(n0 / kBlock) * KB;
+  const int col = n0 + min(r16, valid - 1);  // this lane's weight row
+  const uint8_t* wrow = p.w + (int64_t)col * p.K + g * 32;
+  // Only a tile that is not 16-column aligned (CW = 24) can straddle a
+  // 128-column scale block; the others keep a wave-uniform (scalar) scale.
+  const int64_t ws_base = (int64_t)((CW % 16 ? col : n0) / kBlock) * KB;
 
   // 1. first batch of this wave's weight loads (local k-blocks ks, ks+KS, ...)
   u32x4 wl[kWideBatch][2];
@@ -769,7 +781,7 @@ __global__ __launch_bounds__(64 * NTW * KS) void dense_wide_kernel(DenseArgs p) 
         float v = red[((nt * MT + i) * 64 + lane) * 4 + e];
         for (int q = 1; q < KS; ++q) v += red[(((q * NTW + nt) * MT + i) * 64 + lane) * 4 + e];
         const int row = 16 * i + 4 * g + e;
-        if (row < p.M) store_out<OUT>(p.out, obase + (int64_t)row * p.ldo + n0 + r16, v);
+        if (row < p.M && r16 < valid) store_out<OUT>(p.out, obase + (int64_t)row * p.ldo + n0 + r16, v);
       }
   }
 }
@@ -885,19 +897,49 @@ static void launch_small(const DenseArgs& a, int parts, hipStream_t s) {
     dense_small_kernel<4, OUT, SDT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
 }
 
-template <int MT, int NTW, int KS, int OUT, int SDT, int QX = 0>
+template <int MT, int NTW, int KS, int OUT, int SDT, int QX = 0, int CW = 16 * NTW>
 static bool launch_wide(const DenseArgs& a, int parts, hipStream_t s) {
   const size_t lds = wide_lds_bytes<MT, NTW, KS>(a.kb_per_part);
-  if (lds > 160 * 1024 || a.N % (16 * NTW)) return false;
-  auto kern = dense_wide_kernel<MT, NTW, KS, OUT, SDT, QX>;
+  if (lds > 160 * 1024 || a.N % CW) return false;
+  auto kern = dense_wide_kernel<MT, NTW, KS, OUT, SDT, QX, CW>;
   static bool configured = false;  // attribute set once per instantiation
   if (!configured) {
     hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     configured = true;
   }
-  kern<<<dim3(a.N / (16 * NTW), parts), 64 * NTW * KS, lds, s>>>(a);
+  kern<<<dim3(a.N / CW, parts), 64 * NTW * KS, lds, s>>>(a);
   return true;
+}
+
+// Columns per workgroup of the M <= 16 wide kernel: the widest of 32, 24,
+// 16 and 8 that gives at least about one workgroup per CU over the grid
+// (weights are the bytes that matter there, and a CU's outstanding misses
+// bound its share), else the narrowest that divides N.
+static int wide_columns(int n, int parts) {
+  static const int cus = [] {
+    int dev = 0, c = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+      c = 256;
+    return c;
+  }();
+  for (int cw : {32, 24, 16, 8})
+    if (n % cw == 0 && (int64_t)(n / cw) * parts >= cus - cus / 16) return cw;
+  for (int cw : {8, 16, 24, 32})
+    if (n % cw == 0) return cw;
+  return 32;
+}
+
+// The M <= 16 wide kernel (MT = 1) at the column count wide_columns picks.
+template <int OUT, int SDT, int QX = 0>
+static bool launch_wide_m16(const DenseArgs& a, int parts, hipStream_t s) {
+  switch (wide_columns(a.N, parts)) {
+    case 24: return launch_wide<1, 2, 8, OUT, SDT, QX, 24>(a, parts, s);
+    case 16: return launch_wide<1, 1, 8, OUT, SDT, QX, 16>(a, parts, s);
+    case 8: return launch_wide<1, 1, 8, OUT, SDT, QX, 8>(a, parts, s);
+    default: return launch_wide<1, 2, 8, OUT, SDT, QX>(a, parts, s);
+  }
 }
 
 // Kernel choice by shape (measured on MI355X, K = 2048, N = 6144):
@@ -914,7 +956,7 @@ static void launch_dense_t(const DenseArgs& a, int parts, hipStream_t s) {
     return;
   }
   if (a.M <= 16)
-    done = launch_wide<1, 2, 8, OUT, SDT>(a, parts, s);
+    done = launch_wide_m16<OUT, SDT>(a, parts, s);
   else if (a.M <= 32)
     done = launch_wide<2, 2, 8, OUT, SDT>(a, parts, s);
   else if (a.M <= 64)
@@ -989,6 +1031,10 @@ constexpr int kFusedQuantizeRows = 16;
 
 template <int OUT, int SDT, int QX>
 static bool launch_fused_small_t(const DenseArgs& a, hipStream_t s) {
+  // Every workgroup quantizes the whole slab, so above 8 rows the extra
+  // workgroups of narrower tiles cost more than their smaller weight share
+  // saves (M=16, N=6144: 7.26 us at 32 columns, 7.37 us at 24).
+  if (a.M <= 8) return launch_wide_m16<OUT, SDT, QX>(a, 1, s);
   if (a.M <= 16) return launch_wide<1, 2, 8, OUT, SDT, QX>(a, 1, s);
   return false;
 }

@@ -58,7 +58,36 @@ def test_projection_exact_products_split(dev, m, k, n):
     test_projection_exact_products(dev, m, k, n)
 
 
-@pytest.mark.parametrize("m,k,n", EXACT_CASES[:6] + SPLIT_CASES)
+# Up to 16 rows the wide kernel picks its columns per workgroup from N:
+# 24 at N = 6144 and 7680 (a 16-column tile with 8 valid columns, and tiles
+# straddling 128-column scale blocks), 16 at 4096, 8 at 2048 and below.
+WIDE_CASES = [(1, 2048, 6144), (16, 2048, 6144), (7, 256, 7680), (4, 512, 4096), (16, 1024, 2048)]
+
+
+@pytest.mark.parametrize("m,k,n", WIDE_CASES)
+def test_projection_exact_products_wide(dev, m, k, n):
+    test_projection_exact_products(dev, m, k, n)
+
+
+@pytest.mark.parametrize("m,k,n", WIDE_CASES)
+def test_fp8_linear_fused_equals_quantize_then_gemm(dev, m, k, n):
+    """The one-launch fused path (the wide kernel quantizing its own slab)
+    equals quantize -> projection_partial bit for bit."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(5 * m + n)
+    x = _t(bf16_normal(rng, (m, k)), dev, torch.bfloat16)
+    w, ws = ofp8.quantize_weight_blocks(rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    wt, wst = _t(w, dev), _t(ws, dev)
+    fused = ops.fp8_linear(x, wt, wst)
+    q, qs = ops.quantize(x)
+    ref = ops.projection_partial(q, qs, wt, wst)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, ref)
+
+
+@pytest.mark.parametrize("m,k,n", EXACT_CASES[:6] + SPLIT_CASES + WIDE_CASES)
 def test_projection_varying_scales(dev, m, k, n):
     """Distinct per-row / per-block scales catch a wrong scale index."""
     import torch
