@@ -481,16 +481,19 @@ __global__ __launch_bounds__(dma::THREADS) void dense_dma_kernel(DenseArgs p) {
   plan.as = p.as;
   plan.soff = (uint32_t)min(m0 + (wave & 3) * 64 + lane, p.M - 1) * (uint32_t)KB;
   plan.scales = copies_a;
+  // quarters of the last (partial) tiles that hold no row of A or of B
+  plan.skip = (copies_a ? m0 : n0) + (wave & 3) * 64 >= (copies_a ? p.M : p.N);
 
   const int a_row0 = (wave & 3) * 64, b_row0 = (wave >> 2) * 128;
   const int col0 = n0 + b_row0;
+  const bool live = m0 + a_row0 < p.M && col0 < p.N;  // wave-uniform
   const int64_t ws_base = (int64_t)min(col0 / kBlock, (p.N - 1) / kBlock) * KB;
   dma::Acc acc;
   acc.clear();
   dma::run<false>(plan, acc, a_row0, b_row0, kb0, kb1, lane, [&](int kb) {
     const float w = load_scale_t<SDT>(p.ws, ws_base + kb);
     return float2{w, w};
-  });
+  }, live);
   const int64_t obase = (int64_t)part * p.part_stride + col0;
   dma::store_tile<OUT>(
       acc, p.out, wave, lane, [&](int r) { return m0 + a_row0 + r < p.M && col0 < p.N; },

@@ -85,6 +85,11 @@ struct AffinePlan {
   const float* as;      // activation scales (waves 0-3)
   uint32_t soff;        // this lane's activation-scale offset (row * KB)
   bool scales;          // wave copies activation scales
+  // Every row of the wave's quarter is past the operand: no copies.  Only
+  // honoured by a wave that multiplies nothing (run with live false); the
+  // stage then keeps stale bytes in that quarter, so a wave may set it only
+  // when those rows feed no stored output.
+  bool skip;
   AKAS_DEV const uint8_t* ptr(int i, uint32_t ko) const {
     return src + (min(row0 + 8u * i, lim) * ld + (chunk ^ ((i & 1) << 4)) + ko);
   }
@@ -104,6 +109,7 @@ struct GatherPlan {
   const float* as;
   uint32_t soff;
   bool scales;
+  bool skip;  // as in AffinePlan
   AKAS_DEV const uint8_t* ptr(int i, uint32_t ko) const {
     const int64_t bank = ((alt_mask >> i) & 1u) ? alt_delta : 0;
     return src + bank + (off[i] + ko);
@@ -142,16 +148,23 @@ struct Acc {
 // Multiply stage S into acc and stream k-block kb_next into stage 1-S.
 //   PAIRED: odd n-tiles use weight scale ws1 (gate/up tiles interleaved
 //   16 rows at a time), even n-tiles ws0.
+//   LIVE: false when every output row or column of the wave's 64x128 tile
+//   is past the matrix (a partial last tile); the wave then only issues its
+//   copies, and the live waves have the LDS to themselves.
 // Each n-tile's four products are folded right after their MFMAs: the fold
 // waits for the MFMA results, and the other wave on the SIMD issues its
 // MFMAs meanwhile (keeping the previous products in flight instead costs 16
 // registers and measured no faster).
-template <int S, bool PAIRED, class Plan>
+template <int S, bool PAIRED, bool LIVE, class Plan>
 AKAS_DEV void multiply(const Plan& p, Acc& acc, int a_row0, int b_row0, float ws0, float ws1,
                        int lane, int kb_next) {
   const uint8_t* at = stage_base<S>();
   const uint8_t* bt = at + BM * 128;
   const uint32_t ko = (uint32_t)kb_next * 128;
+  if constexpr (!LIVE) {
+    if (!p.skip) copy_stage<1 - S>(p, kb_next);
+    return;
+  }
   v8i af[4];
   float c0[4], c1[4];
 #pragma unroll
@@ -186,24 +199,32 @@ AKAS_DEV void multiply(const Plan& p, Acc& acc, int a_row0, int b_row0, float ws
 // as a float2.  Every stage refills the other one with k-block
 // min(kb + 1, kb1 - 1): the refetch of the last block lands in a stage that
 // is never read again, and the closing barrier waits for it.
-template <bool PAIRED, class Plan, class WS>
-AKAS_DEV void run(const Plan& p, Acc& acc, int a_row0, int b_row0, int kb0, int kb1, int lane, WS ws) {
-  copy_stage<0>(p, kb0);
+template <bool PAIRED, bool LIVE, class Plan, class WS>
+AKAS_DEV void run_(const Plan& p, Acc& acc, int a_row0, int b_row0, int kb0, int kb1, int lane, WS ws) {
+  if (LIVE || !p.skip) copy_stage<0>(p, kb0);
   float2 wcur = ws(kb0);
   __syncthreads();
   const int last = kb1 - 1;
   for (int kb = kb0; kb < kb1; kb += 2) {
     float2 wnext = ws(min(kb + 1, last));
-    multiply<0, PAIRED>(p, acc, a_row0, b_row0, wcur.x, wcur.y, lane, min(kb + 1, last));
+    multiply<0, PAIRED, LIVE>(p, acc, a_row0, b_row0, wcur.x, wcur.y, lane, min(kb + 1, last));
     __syncthreads();
     if (kb + 1 < kb1) {
       wcur = wnext;
       wnext = ws(min(kb + 2, last));
-      multiply<1, PAIRED>(p, acc, a_row0, b_row0, wcur.x, wcur.y, lane, min(kb + 2, last));
+      multiply<1, PAIRED, LIVE>(p, acc, a_row0, b_row0, wcur.x, wcur.y, lane, min(kb + 2, last));
       __syncthreads();
       wcur = wnext;
     }
   }
+}
+template <bool PAIRED, class Plan, class WS>
+AKAS_DEV void run(const Plan& p, Acc& acc, int a_row0, int b_row0, int kb0, int kb1, int lane, WS ws,
+                  bool live) {
+  if (live)  // wave-uniform: two loops, so the live one keeps its registers
+    run_<PAIRED, true>(p, acc, a_row0, b_row0, kb0, kb1, lane, ws);
+  else
+    run_<PAIRED, false>(p, acc, a_row0, b_row0, kb0, kb1, lane, ws);
 }
 
 AKAS_DEV uint32_t pack2(float lo, float hi, int dt) {

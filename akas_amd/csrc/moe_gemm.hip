@@ -527,6 +527,7 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
     }
     plan.soff = (uint32_t)rows_src[(wave & 3) * 64 + lane] * (uint32_t)KB;
     plan.scales = true;
+    plan.skip = row0 + (wave & 3) * 64 >= count;  // a quarter of padding rows only
   } else {
     const int64_t ebase = (int64_t)e * p.N * p.K;
     plan.src = p.w + ebase;
@@ -540,6 +541,7 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
     }
     plan.soff = 0;
     plan.scales = false;
+    plan.skip = false;
   }
 
   const int wm = wave & 3, wn = wave >> 2;
@@ -551,7 +553,7 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
   acc.clear();
   dma::run<PAIRED>(plan, acc, a_row0, b_row0, kb0, kb1, lane, [&](int kb) {
     return float2{load_scale_t<SDT>(p.ws, ws_base + kb), PAIRED ? load_scale_t<SDT>(p.ws2, ws_base + kb) : 0.f};
-  });
+  }, row0 + a_row0 < count);  // a wave whose 64 rows are all padding only copies
 
   if constexpr (!PAIRED) {
     const int64_t rstride = (int64_t)p.parts * p.N;
