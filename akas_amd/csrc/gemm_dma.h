@@ -44,6 +44,10 @@ static __shared__ __attribute__((aligned(1024))) uint8_t stage0[STAGE];
 static __shared__ __attribute__((aligned(1024))) uint8_t stage1[STAGE];
 static __shared__ __attribute__((aligned(16))) float scales0[BM];
 static __shared__ __attribute__((aligned(16))) float scales1[BM];
+// Weight scales of a tile's two 128-row B blocks, one per k-block of the
+// workgroup's k range (at most MAX_KB k-blocks).
+constexpr int MAX_KB = 128;
+static __shared__ __attribute__((aligned(16))) float wtab[2][MAX_KB];
 
 template <int S> AKAS_DEV uint8_t* stage_base() { return S ? stage1 : stage0; }
 template <int S> AKAS_DEV float* stage_scales() { return S ? scales1 : scales0; }

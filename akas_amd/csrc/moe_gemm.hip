@@ -476,7 +476,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
 // stay in L2 across its column blocks and neighbouring row tiles of one
 // expert share its weights.
 // ---------------------------------------------------------------------------
-template <int MODE, int OUT, int SDT>
+template <int MODE, int OUT>
 __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) {
   constexpr bool PAIRED = paired_mode(MODE);
   constexpr int BM = dma::BM;
@@ -510,6 +510,18 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
     int dst = -1;
     if (live) dst = p.packed_out ? p.offsets[e] + idx : p.routes[(int64_t)e * p.r + idx];
     rows_dst[i] = dst < p.out_rows ? dst : -1;
+  }
+  // Weight scales over the k range as float32 (either scale dtype gives the
+  // same main loop): PAIRED, gate (h = 0) and up (h = 1) of the tile's one
+  // 128-column block; else the tile's two column blocks.
+  const int nkb = kb1 - kb0;
+  for (int i = tid; i < 2 * nkb; i += dma::THREADS) {
+    const int h = i / nkb, k = kb0 + i % nkb;
+    const void* src = (PAIRED && h) ? p.ws2 : p.ws;
+    const int cb = PAIRED ? n0 / kBlock : min((n0 + 128 * h) / kBlock, NB - 1);
+    const int64_t at = ((int64_t)e * NB + cb) * KB + k;
+    dma::wtab[h][i % nkb] = p.ws_dtype == AKAS_DTYPE_F32 ? load_scale_t<AKAS_DTYPE_F32>(src, at)
+                                                         : load_scale_t<AKAS_DTYPE_BF16>(src, at);
   }
   __syncthreads();
 
@@ -548,11 +560,12 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
   const int a_row0 = wm * 64, b_row0 = wn * 128;
   // First output column of this wave; gate and up share its scale block.
   const int wcol = PAIRED ? n0 + b_row0 / 2 : n0 + b_row0;
-  const int64_t ws_base = ((int64_t)e * NB + wcol / kBlock) * KB;
+  const float* w0 = dma::wtab[PAIRED ? 0 : wn] - kb0;
+  const float* w1 = dma::wtab[1] - kb0;
   dma::Acc acc;
   acc.clear();
   dma::run<PAIRED>(plan, acc, a_row0, b_row0, kb0, kb1, lane, [&](int kb) {
-    return float2{load_scale_t<SDT>(p.ws, ws_base + kb), PAIRED ? load_scale_t<SDT>(p.ws2, ws_base + kb) : 0.f};
+    return float2{w0[kb], PAIRED ? w1[kb] : 0.f};
   }, row0 + a_row0 < count);  // a wave whose 64 rows are all padding only copies
 
   if constexpr (!PAIRED) {
@@ -724,16 +737,14 @@ static void launch_expert_dma(ExpertArgs a, hipStream_t s) {
   a.max_tiles = (int)capacity_tiles(a.r, a.top, a.E, dma::BM);
   a.tiles_n = paired_mode(MODE) ? a.N / (dma::BN / 2) : a.N / dma::BN;
   dim3 grid((unsigned)(a.max_tiles * a.tiles_n), (unsigned)a.parts);
-  if (a.ws_dtype == AKAS_DTYPE_F32)
-    expert_dma_kernel<MODE, OUT, AKAS_DTYPE_F32><<<grid, dma::THREADS, 0, s>>>(a);
-  else
-    expert_dma_kernel<MODE, OUT, AKAS_DTYPE_BF16><<<grid, dma::THREADS, 0, s>>>(a);
+  expert_dma_kernel<MODE, OUT><<<grid, dma::THREADS, 0, s>>>(a);
 }
 
 // Experts holding hundreds of rows on average (prefill batches) take the
 // DMA-fed 256-row tiles; its 16-byte stores need a 16-byte aligned output.
 static bool expert_dma_fits(const ExpertArgs& a, int64_t mean, int64_t n_mult) {
-  return mean >= 128 && a.N % n_mult == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0;
+  return mean >= 128 && a.N % n_mult == 0 && a.kb_per_part <= dma::MAX_KB &&
+         reinterpret_cast<uintptr_t>(a.out) % 16 == 0;
 }
 
 // Row tile by the mean rows per expert: 32-row tiles for decode-like batches,

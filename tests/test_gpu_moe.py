@@ -336,14 +336,17 @@ def _expert_case(rng, rows, top, experts, o, k, routed, exact=True, mult=1):
     # and routed rows, N = 256 and 512, and N = 384 on the 128-row fallback)
     (1500, 2, 6, 512, 384, True), (700, 4, 16, 256, 512, False), (600, 3, 5, 384, 256, False)])
 def test_expert_partial_exact(dev, rows, top, experts, o, k, routed):
+    import torch
     from akas_amd import ops
 
     rng = np.random.default_rng(37)
     ids, active, counts, routes, x, xs, w, ws = _expert_case(rng, rows, top, experts, o, k, routed)
-    out = ops.expert_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev), _t(counts, dev),
-                             _t(routes, dev), r=rows, top=top, routed_input=routed)
     exp = omoe.expert_partial(x, xs, w, ws, counts, routes, top, routed_input=routed)
-    np.testing.assert_array_equal(_np(out), exp)
+    for sdt in (torch.float32, torch.bfloat16):  # binary scales are exact in bf16
+        out = ops.expert_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev, sdt),
+                                 _t(counts, dev), _t(routes, dev), r=rows, top=top,
+                                 routed_input=routed)
+        np.testing.assert_array_equal(_np(out), exp)
 
 
 @pytest.mark.parametrize("rows", [257, 1200])
@@ -622,7 +625,9 @@ def test_expert_pair_partial_exact(dev, rows, top, experts, o, k, parts):
     """Exact products (codes {56, 64} with sign, binary scales; the up
     weights are the flipped gate weights, as in the reference's
     paired_partial_validation): gate and up partials equal the oracle bit
-    for bit; unrouted entries are untouched."""
+    for bit with float32 and with bfloat16 weight scales; unrouted entries
+    are untouched."""
+    import torch
     from akas_amd import ops
 
     rng = np.random.default_rng(905)
@@ -632,12 +637,13 @@ def test_expert_pair_partial_exact(dev, rows, top, experts, o, k, parts):
     xs = (2.0 ** rng.integers(-4, 2, (rows, k // 128))).astype(np.float32)
     ws = (2.0 ** rng.integers(-4, 2, (experts, o // 128, k // 128))).astype(np.float32)
     w2, ws2 = np.flip(w, axis=-2).copy(), np.flip(ws, axis=-1).copy()
-    gate, up = ops.expert_pair_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev),
-                                       _t(w2, dev), _t(ws2, dev), _t(counts, dev), _t(routes, dev),
-                                       r=rows, top=top, partitions=parts)
     eg, eu = omoe.expert_pair_partial(x, xs, w, ws, w2, ws2, counts, routes, top, parts)
-    np.testing.assert_array_equal(_np(gate), eg)
-    np.testing.assert_array_equal(_np(up), eu)
+    for sdt in (torch.float32, torch.bfloat16):  # binary scales are exact in bf16
+        gate, up = ops.expert_pair_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev, sdt),
+                                           _t(w2, dev), _t(ws2, dev, sdt), _t(counts, dev),
+                                           _t(routes, dev), r=rows, top=top, partitions=parts)
+        np.testing.assert_array_equal(_np(gate), eg)
+        np.testing.assert_array_equal(_np(up), eu)
 
 
 @pytest.mark.parametrize("rows,parts", [(1, 2), (40, 3), (1200, 2)])
