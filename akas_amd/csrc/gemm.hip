@@ -911,16 +911,44 @@ static void launch_small(const DenseArgs& a, int parts, hipStream_t s) {
     dense_small_kernel<4, OUT, SDT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
 }
 
+// Host-side state kept per device (the current one when a call launches).
+constexpr int kMaxDevices = 64;
+
+static int current_device() {
+  int dev = -1;
+  return hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices ? dev : -1;
+}
+
+// Compute units of the current device (256 when they cannot be read).
+static int device_cus() {
+  static std::atomic<int> cus[kMaxDevices];
+  const int dev = current_device();
+  if (dev < 0) return 256;
+  int c = cus[dev].load(std::memory_order_relaxed);
+  if (c > 0) return c;
+  if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+    c = 256;
+  cus[dev].store(c, std::memory_order_relaxed);
+  return c;
+}
+
+// Returns false (the caller takes another kernel) when the tile does not
+// fit or the kernel's dynamic LDS limit cannot be raised on this device.
 template <int MT, int NTW, int KS, int OUT, int SDT, int QX = 0, int CW = 16 * NTW>
 static bool launch_wide(const DenseArgs& a, int parts, hipStream_t s) {
   const size_t lds = wide_lds_bytes<MT, NTW, KS>(a.kb_per_part);
   if (lds > 160 * 1024 || a.N % CW) return false;
   auto kern = dense_wide_kernel<MT, NTW, KS, OUT, SDT, QX, CW>;
-  static bool configured = false;  // attribute set once per instantiation
-  if (!configured) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    configured = true;
+  // The 160 KB dynamic LDS limit, raised once per device for this kernel
+  // (bit d: done on device d).
+  static std::atomic<uint64_t> configured{0};
+  const int dev = current_device();
+  if (dev < 0) return false;
+  if (!((configured.load(std::memory_order_acquire) >> dev) & 1u)) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+      return false;
+    configured.fetch_or(uint64_t{1} << dev, std::memory_order_release);
   }
   kern<<<dim3(a.N / CW, parts), 64 * NTW * KS, lds, s>>>(a);
   return true;
@@ -931,13 +959,7 @@ static bool launch_wide(const DenseArgs& a, int parts, hipStream_t s) {
 // (weights are the bytes that matter there, and a CU's outstanding misses
 // bound its share), else the narrowest that divides N.
 static int wide_columns(int n, int parts) {
-  static const int cus = [] {
-    int dev = 0, c = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
-      c = 256;
-    return c;
-  }();
+  const int cus = device_cus();
   for (int cw : {32, 24, 16, 8})
     if (n % cw == 0 && (int64_t)(n / cw) * parts >= cus - cus / 16) return cw;
   for (int cw : {8, 16, 24, 32})
@@ -1187,15 +1209,14 @@ extern "C" int akas_fp8_linear(const void* x, int x_dtype, const uint8_t* w, con
 // ---------------------------------------------------------------------------
 static __device__ __align__(256) uint8_t scratch[AKAS_NOALLOC_SCRATCH_BYTES];
 
-constexpr int kMaxDevices = 64;
 static std::atomic<void*> scratch_address[kMaxDevices];
 static std::mutex scratch_mutex;
 
 // Device address of the current device's `scratch`, or null when the device
 // index is out of range or the runtime cannot resolve the symbol.
 static void* current_scratch() {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  const int dev = current_device();
+  if (dev < 0) return nullptr;
   void* p = scratch_address[dev].load(std::memory_order_acquire);
   if (p) return p;
   std::lock_guard<std::mutex> lock(scratch_mutex);
