@@ -238,7 +238,12 @@ def prefill_gemms(torch, dev, steps):
 LAYERS_PER_GRAPH = 4  # MoE blocks captured back to back in one graph
 
 
-def moe_layer_bench(torch, dev, tokens, zipf, steps):
+def moe_layer_bench(torch, dev, tokens, zipf, steps, packed=False):
+    """The routed MoE block (router, routes, grouped gate/up with SwiGLU and
+    re-quantize, grouped down, combine).  packed: the reference's packed
+    policy (an expert_pack copy, then contiguous expert rows); unpacked, the
+    grouped kernels gather each expert's rows through the route table
+    themselves, with bit-identical outputs."""
     from akas_amd import moe
 
     H, F, E, top = 2048, 1536, 64, 4
@@ -254,7 +259,6 @@ def moe_layer_bench(torch, dev, tokens, zipf, steps):
     if zipf:
         logits += (-1.1 * np.log1p(rng.permutation(E))).astype(np.float32)[None, :]
     logits = torch.from_numpy(logits).to(dev)
-    packed = tokens >= 2048
     fn = lambda i: moe.routed_moe(x, logits, None, wts, top=top, packed=packed,
                                   max_block_m=128 if packed else 64,
                                   product_dtype=torch.bfloat16, activation_dtype=torch.bfloat16,
@@ -271,7 +275,7 @@ def moe_layer_bench(torch, dev, tokens, zipf, steps):
     wbytes = active_experts * 3 * F * H
     abytes = 2 * tokens * H + tokens * H + tokens * top * (H + F) + tokens * top * H * 2 + 2 * tokens * H
     del bank, wts
-    return dict(T=tokens, zipf=zipf, us=round(ms * 1e3, 2),
+    return dict(T=tokens, zipf=zipf, packed=packed, us=round(ms * 1e3, 2),
                 tflops=round(flops / (ms * 1e-3) / 1e12, 1),
                 gbs=round((wbytes + abytes) / (ms * 1e-3) / 1e9, 1),
                 frac_hbm=round((wbytes + abytes) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -512,11 +516,10 @@ def kernel_probe(torch, dev, what):
         if zipf:
             logits += (-1.1 * np.log1p(rng.permutation(E))).astype(np.float32)[None, :]
         logits = torch.from_numpy(logits).to(dev)
-        packed = tokens >= 2048
-        for _ in range(3):
-            moe.routed_moe(x, logits, None, wts, top=4, packed=packed,
-                           max_block_m=128 if packed else 64, product_dtype=torch.bfloat16,
-                           activation_dtype=torch.bfloat16, contribution_dtype=torch.bfloat16)
+        for _ in range(3):  # unpacked, as the bench line's MoE layers
+            moe.routed_moe(x, logits, None, wts, top=4, packed=False, max_block_m=64,
+                           product_dtype=torch.bfloat16, activation_dtype=torch.bfloat16,
+                           contribution_dtype=torch.bfloat16)
         info.update(op=f"routed MoE layer T={tokens}{' zipf' if zipf else ''}, x3",
                     flops=6 * F * H * tokens * 4)
     elif what != "copy":
@@ -670,6 +673,7 @@ def main():
             prefill_gemm=prefill,
             moe_decode=moe_layer_bench(torch, dev, 256, False, 20),
             moe_prefill_zipf=moe_layer_bench(torch, dev, 16384, True, 10),
+            moe_prefill_zipf_packed=moe_layer_bench(torch, dev, 16384, True, 10, packed=True),
             rms_quantize=rms_quantize_bench(torch, dev),
             shared_expert_moe_decode=shared_expert_block_bench(torch, dev))
     if not args.no_cpu:
