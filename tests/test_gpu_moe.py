@@ -1009,7 +1009,8 @@ def test_routed_moe_layer_lfm2_dims(dev, lfm2_bank, rows, packed, zipf):
 def test_routed_moe_layer_zipf_prefill_full_size(dev, lfm2_bank):
     """The skewed prefill batch of the benchmark: T = 16384 tokens, Zipf(1.1)
     per-expert logit offsets, packed 128-aligned experts on the DMA-fed
-    256-row tiles (the top expert holds about 14.6k routed rows, 57 tiles).
+    256-row tiles (the top expert holds about 14.6k routed rows, 57 tiles),
+    and the unpacked policy bit-identical to it.
     The whole batch runs on the device; the routes are compared in full and
     the layer output on a token sample holding, for every live expert, its
     first two and last two routed tokens, plus every token of the largest
@@ -1051,6 +1052,12 @@ def test_routed_moe_layer_zipf_prefill_full_size(dev, lfm2_bank):
     assert np.isfinite(got).all()
     norms = np.linalg.norm(got, axis=1)
     assert 0.5 < np.median(norms) / np.median(np.linalg.norm(exp, axis=1)) < 2.0
+    # unpacked (the benchmark's policy: rows gathered through the route
+    # table by the grouped kernels) gives the same bits on every token
+    flat = moe.routed_moe(_t(x, dev, bf), _t(logits, dev), None, wts, top=top, packed=False,
+                          max_block_m=64, product_dtype=bf, activation_dtype=bf,
+                          contribution_dtype=bf)
+    np.testing.assert_array_equal(_np(flat), got)
 
 
 # ---------------------------------------------------------------------------
