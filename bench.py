@@ -533,7 +533,10 @@ def roofline_ceilings(torch, dev):
     """The GPU's measured ceilings from the probe library: a streaming read
     of 1 GiB (four times the 256 MB last-level cache) at several grid sizes,
     and back-to-back FP8 MFMAs at 8 waves per SIMD; each the best of 5 timed
-    launches (HIP events on the launching stream)."""
+    launches (HIP events on the launching stream).  Also the floor of one
+    decode op: a pure read of one N x K weight matrix of the sweep in one
+    launch, graph-replayed back to back over copies rotated past the
+    last-level cache as the sweep's weights are (best grid)."""
     import ctypes
 
     from akas_amd import build
@@ -555,6 +558,16 @@ def roofline_ceilings(torch, dev):
         gbs = nbytes / (ms * 1e-3) / 1e9
         best_read = max(best_read, (gbs, blocks))
     del buf
+    wbytes, copies = N_DEC * K_DEC, 48
+    wbufs = torch.ones((copies, wbytes // 4), dtype=torch.float32, device=dev)
+    best_op = (float("inf"), 0)
+    for blocks in (256, 512, 768, 1024, 2048):
+        sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+        ms = time_kernel_graph(torch, lambda i: lib.akas_probe_stream_read(
+            wbufs[i % copies].data_ptr(), wbytes, sink.data_ptr(), blocks,
+            torch.cuda.current_stream().cuda_stream), copies)
+        best_op = min(best_op, (ms * 1e3, blocks))
+    del wbufs
     iters, blocks = 4000, 256 * 8
     sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
@@ -564,6 +577,9 @@ def roofline_ceilings(torch, dev):
                 hbm_read_frac_of_peak=round(best_read[0] / HBM_PEAK_GBS, 4),
                 mfma_fp8_tflops=round(tflops, 1),
                 mfma_fp8_frac_of_peak=round(tflops / FP8_PEAK_TFLOPS, 4),
+                decode_weight_read_us=round(best_op[0], 3), decode_weight_read_grid=best_op[1],
+                decode_weight_read_gbs=round(wbytes / (best_op[0] * 1e-6) / 1e9, 1),
+                decode_step_read_floor_us=round(len(DECODE_M) * best_op[0], 3),
                 source="akas_amd/csrc/probe/roofline.hip")
 
 
