@@ -498,11 +498,11 @@ __global__ __launch_bounds__(dma::THREADS) void dense_dma_kernel(DenseArgs p) {
                                                          : load_scale_t<AKAS_DTYPE_BF16>(p.ws, at);
   }
   __syncthreads();
-  const float* wrow = dma::wtab[wave >> 2] - kb0;
+  const float* wrow = dma::wtab[wave >> 2];
   dma::Acc acc;
   acc.clear();
   dma::run<false>(plan, acc, a_row0, b_row0, kb0, kb1, lane, [&](int kb) {
-    const float w = wrow[kb];
+    const float w = wrow[kb - kb0];
     return float2{w, w};
   }, live);
   const int64_t obase = (int64_t)part * p.part_stride + col0;

@@ -560,12 +560,12 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
   const int a_row0 = wm * 64, b_row0 = wn * 128;
   // First output column of this wave; gate and up share its scale block.
   const int wcol = PAIRED ? n0 + b_row0 / 2 : n0 + b_row0;
-  const float* w0 = dma::wtab[PAIRED ? 0 : wn] - kb0;
-  const float* w1 = dma::wtab[1] - kb0;
+  const float* w0 = dma::wtab[PAIRED ? 0 : wn];
+  const float* w1 = dma::wtab[1];
   dma::Acc acc;
   acc.clear();
   dma::run<PAIRED>(plan, acc, a_row0, b_row0, kb0, kb1, lane, [&](int kb) {
-    return float2{w0[kb], PAIRED ? w1[kb] : 0.f};
+    return float2{w0[kb - kb0], PAIRED ? w1[kb - kb0] : 0.f};
   }, row0 + a_row0 < count);  // a wave whose 64 rows are all padding only copies
 
   if constexpr (!PAIRED) {
