@@ -398,7 +398,7 @@ def cpu_baseline():
 
     linear_case(16, 2048, 2048, "config1_linear_m16", "full: x [16, 2048], W [2048, 2048]")
     linear_case(256, 2048, 6144, "config3_prefill_gemm",
-                "256 of the 8192 rows of M=8192, K=2048, N=6144 (rate scales with rows)", 3)
+                "256 of the 8192 rows of M=8192, K=2048, N=6144 (rate scales with rows)")
 
     # config 2, the headline's baseline: the full sweep
     w = rng.normal(0, 0.02, (N_DEC, K_DEC)).astype(np.float32)
@@ -412,7 +412,7 @@ def cpu_baseline():
                                     nthreads)
 
     med, runs = _median_time(lambda: sweep(threads), 5, 8.0)
-    med1, _ = _median_time(lambda: sweep(1), 3, 0.0)
+    med1, runs1 = _median_time(lambda: sweep(1), 5, 0.0)
     step_bytes = sum(dense_bytes(m, K_DEC, N_DEC) for m in DECODE_M)
 
     # configs 4 and 5: the MoE layer (H=2048, F=1536, 64 experts, top 4)
@@ -434,16 +434,16 @@ def cpu_baseline():
         per[label] = dict(ms=round(t * 1e3, 2), gflops=round(flops / t / 1e9, 2), runs=count,
                           sample=sample)
 
-    moe_case(256, False, "config4_moe_decode", "full: T=256, all 64 experts active", 3)
+    moe_case(256, False, "config4_moe_decode", "full: T=256, all 64 experts active", 5)
     moe_case(512, True, "config5_moe_prefill_zipf",
-             "512 of the 16384 tokens, same Zipf(1.1) logit offsets (rate scales with tokens)", 2)
+             "512 of the 16384 tokens, same Zipf(1.1) logit offsets (rate scales with tokens)", 5)
     return dict(value=round(step_bytes / med / 1e9, 3), unit="GB/s", cores=threads, kind="port",
                 cpu_model=_cpu_model(), host_cpus=os.cpu_count(),
                 sample=f"full decode sweep (M=1,4,16,64,256; K=2048; N=6144), median of {runs} "
                        f"runs, {med * 1e3:.1f} ms/sweep, oracle/cpu_ref.c -O3 -fopenmp, f32 "
                        f"accumulation",
                 value_1_thread=round(step_bytes / med1 / 1e9, 3),
-                sample_1_thread=f"same sweep on 1 thread, median of 3 runs, "
+                sample_1_thread=f"same sweep on 1 thread, median of {runs1} runs, "
                                 f"{med1 * 1e3:.1f} ms/sweep",
                 per_config=per)
 
