@@ -28,7 +28,8 @@ def bf16_round(values):
 
 def f16_round(values):
     """Round float32 to float16 and back (IEEE nearest-even)."""
-    return np.asarray(values, dtype=np.float32).astype(np.float16).astype(np.float32)
+    with np.errstate(over="ignore"):  # beyond the f16 range rounds to inf, as in IEEE
+        return np.asarray(values, dtype=np.float32).astype(np.float16).astype(np.float32)
 
 
 def round_to(values, dtype):
@@ -82,7 +83,8 @@ def encode_e4m3(values):
     magnitude = np.abs(v)
     rounded = (bits & np.uint32(0x7FFFFFFF)) + np.uint32(0x7FFFF) + ((bits >> 20) & 1)
     normal = (rounded >> 20).astype(np.int64) - 960
-    subnormal = np.rint(magnitude * np.float32(512)).astype(np.int64)
+    with np.errstate(over="ignore", invalid="ignore"):  # only taken below 2^-6
+        subnormal = np.rint(magnitude * np.float32(512)).astype(np.int64)
     code = np.clip(np.where(magnitude < np.float32(0.015625), subnormal, normal), 0, 126)
     return code.astype(np.uint8) | ((bits >> 24) & 128).astype(np.uint8)
 
@@ -118,7 +120,8 @@ def quantize(x):
         raise ValueError("FP8 channels must be divisible by 128")
     blocks = x.reshape(*x.shape[:-1], k // BLOCK, BLOCK)
     scales = group_scales(blocks)
-    codes = encode_e4m3(blocks / scales[..., None]).reshape(x.shape)
+    with np.errstate(invalid="ignore"):  # inf / inf in a group holding inf gives NaN, as on the GPU
+        codes = encode_e4m3(blocks / scales[..., None]).reshape(x.shape)
     return codes, scales
 
 

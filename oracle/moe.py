@@ -356,7 +356,8 @@ def swiglu(gate, up, round_dtype=None):
     u = np.asarray(up, np.float32)
     if round_dtype is not None:
         g, u = round_to(g, round_dtype), round_to(u, round_dtype)
-    return (g / (np.float32(1) + np.exp(-g)) * u).astype(np.float32)
+    with np.errstate(over="ignore"):  # exp(-g) = inf for g < -88: the quotient is -0
+        return (g / (np.float32(1) + np.exp(-g)) * u).astype(np.float32)
 
 
 def swiglu_experts(gate, up, round_inputs=False, round_dtype="float32", output_dtype="float32"):
@@ -452,7 +453,8 @@ def fp8_expert_swiglu(x, activation_scales, w, scales, w2, scales2, counts, rout
         c = owners.size
         blocks = act.reshape(c, o // BLOCK, BLOCK)
         s = group_scales(blocks)
-        q = (blocks / s[..., None]).astype(np.float32)
+        with np.errstate(invalid="ignore"):  # inf / inf for a group holding inf
+            q = (blocks / s[..., None]).astype(np.float32)
         normalized[owners, ranks] = q.reshape(c, o)
         codes[owners, ranks] = encode_e4m3(q).reshape(c, o)
         out_scales[owners, ranks] = s

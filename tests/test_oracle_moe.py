@@ -376,7 +376,8 @@ def test_fused_swiglu_against_float64_and_composition(pd, ad):
             u = ofp8.round_to(_int_products(x[row][None], xs[row][None], w2[e], ws[e]).astype(np.float32), pd)
             a = ofp8.round_to((g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u).astype(np.float32), ad)
             s = (np.maximum(np.abs(a.reshape(-1, 128)).max(-1), 1e-12) / 448).astype(np.float32)
-            q = (a.reshape(-1, 128).astype(np.float64) / s[:, None]).astype(np.float32).reshape(-1)
+            with np.errstate(invalid="ignore"):  # inf / inf in a group holding inf
+                q = (a.reshape(-1, 128).astype(np.float64) / s[:, None]).astype(np.float32).reshape(-1)
             ok = omoe.codes_within_midpoint_band(codes[row, rank], ofp8.encode_e4m3(q), q)
             assert ok.all()
             np.testing.assert_allclose(scales[row, rank], s, rtol=2e-6)
