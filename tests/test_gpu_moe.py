@@ -1286,6 +1286,40 @@ def test_routed_moe_layer_graph_replays(dev, packed, fused_combine):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("fused_combine", [False, True])
+def test_routed_moe_two_streams(dev, fused_combine):
+    """The routed block called on two streams at once, on different inputs,
+    repeatedly: the per-stream caches (workspaces, the fused combine's
+    arrival counters) keep the calls apart, and every result equals the
+    one-stream result bit for bit."""
+    import torch
+    from akas_amd import moe
+
+    rows, H, F, E, top = 300, 512, 256, 16, 4
+    rng = np.random.default_rng(99)
+    bank = {}
+    for name, shape in (("w1", (E, F, H)), ("w3", (E, F, H)), ("w2", (E, H, F))):
+        bank[name] = ofp8.quantize_weight_blocks(rng.normal(0, 0.05, shape).astype(np.float32))
+    wts = moe.ExpertWeights(*(_t(a, dev) for n in ("w1", "w3", "w2") for a in bank[n]))
+    xs = [_t(bf16_normal(rng, (rows, H)), dev, torch.bfloat16) for _ in range(2)]
+    logits = [_t(rng.normal(0, 1, (rows, E)).astype(np.float32), dev) for _ in range(2)]
+    kw = dict(top=top, fused_combine=fused_combine)
+    ref = [moe.routed_moe(x, lg, None, wts, **kw).clone() for x, lg in zip(xs, logits)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    outs = [[] for _ in streams]
+    for rep in range(10):
+        for j, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                outs[j].append(moe.routed_moe(xs[j], logits[j], None, wts, **kw))
+    torch.cuda.synchronize()
+    for j in range(len(streams)):
+        for out in outs[j]:
+            np.testing.assert_array_equal(_np(out), _np(ref[j]))
+
+
 @pytest.mark.parametrize("rows,experts,top,k,x_dtype,softmax,with_bias", [
     (1, 64, 4, 2048, "bfloat16", True, False), (257, 64, 4, 2048, "float32", False, True),
     (16384, 64, 4, 2048, "bfloat16", True, True), (33, 32, 6, 512, "float16", False, False),
