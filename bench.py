@@ -225,8 +225,12 @@ def prefill_gemms(torch, dev, steps):
         ms_gemm = time_kernel(torch, lambda i: ops.projection_partial(
             q, qs, codes[0], scales[0], out=out, out_dtype=torch.bfloat16), steps)
         flops = 2 * m * k * n
+        # the same GEMM with bf16 weight scales (the block-FP8 checkpoints' dtype)
+        scales_bf16 = scales[0].to(torch.bfloat16)
+        ms_bf16 = time_kernel(torch, lambda i: ops.projection_partial(
+            q, qs, codes[0], scales_bf16, out=out, out_dtype=torch.bfloat16), steps)
         res.append(dict(M=m, K=k, N=n, op_us=round(ms_total * 1e3, 2),
-                        gemm_us=round(ms_gemm * 1e3, 2),
+                        gemm_us=round(ms_gemm * 1e3, 2), gemm_bf16_scales_us=round(ms_bf16 * 1e3, 2),
                         op_tflops=round(flops / (ms_total * 1e-3) / 1e12, 1),
                         gemm_tflops=round(flops / (ms_gemm * 1e-3) / 1e12, 1),
                         op_frac_fp8=round(flops / (ms_total * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
