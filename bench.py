@@ -207,7 +207,8 @@ PREFILL_SHAPES = ((2048, 6144), (2048, 8192), (8192, 2048))
 def prefill_gemms(torch, dev, steps):
     """Config 3: M=8192, fused activation quantize, bf16 out.  ``op``: the
     fp8_linear call (all its launches); ``gemm``: its GEMM launch alone, on
-    prequantized codes (the same kernel)."""
+    prequantized codes (the same kernel); ``gemm_bf16_scales``: that launch
+    with the weight scales in bf16."""
     from akas_amd import ops
 
     res = []
