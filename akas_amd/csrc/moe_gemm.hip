@@ -227,9 +227,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
   using Plan = StagePlan<BM, BN, THREADS>;
   constexpr int STAGE = (BM + BN) * 128;
   // The 32-row expert partial (the decode down projection) keeps one LDS
-  // stage: 20.9 KB lets four workgroups share a CU instead of three, 38.6 ->
-  // 36.6 us at 64 experts x 1536 -> 2048.  The paired gate/up kernel was
-  // slower that way (86.8 -> 90.6 us) and keeps two.
+  // stage: 20.9 KB (128 columns) or 36.9 KB (256) lets four workgroups share
+  // a CU instead of three, 38.6 -> 36.6 us at 64 experts x 1536 -> 2048 with
+  // 128 columns.  The paired gate/up kernel was slower that way (86.8 -> 90.6
+  // us) and keeps two.
   constexpr int NSTAGE = (!PAIRED && BM == 32) ? 1 : 2;
   __shared__ __attribute__((aligned(16))) uint8_t lds[NSTAGE * STAGE];
   __shared__ __attribute__((aligned(16))) float lds_as[NSTAGE][BM];
@@ -752,7 +753,12 @@ static bool expert_dma_fits(const ExpertArgs& a, int64_t mean, int64_t n_mult) {
 template <int OUT, int MODE = kPartial>
 static void launch_partial(const ExpertArgs& a, hipStream_t s) {
   const int64_t mean = (int64_t)a.r * a.top / a.E;
-  if (mean <= 48)
+  // 256-column tiles where N allows: half the workgroups of 128-column ones,
+  // each streaming twice the weights (LFM2 decode layer 146.0 -> 145.0 us,
+  // the Qwen3.5 block 191.9 -> 189.2 us; 512 columns was slower).
+  if (mean <= 48 && a.N % 256 == 0)
+    launch_expert<32, 256, 1, 4, MODE, OUT>(a, s);
+  else if (mean <= 48)
     launch_expert<32, 128, 1, 4, MODE, OUT>(a, s);
   else if (expert_dma_fits(a, mean, dma::BN))
     launch_expert_dma<MODE, OUT>(a, s);

@@ -332,6 +332,8 @@ def _expert_case(rng, rows, top, experts, o, k, routed, exact=True, mult=1):
     (3, 2, 4, 128, 256, False), (1, 4, 64, 128, 256, False), (33, 2, 4, 128, 256, False),
     (33, 2, 4, 128, 384, True), (257, 3, 7, 256, 384, True), (256, 4, 64, 256, 512, False),
     (2048, 4, 8, 256, 256, False),
+    # 32-row tiles with 256 columns (N % 256 == 0), routed input, N = 768
+    (200, 4, 32, 768, 256, True),
     # >= 128 rows per expert: 256-row DMA tiles (ragged last tiles, gathered
     # and routed rows, N = 256 and 512, and N = 384 on the 128-row fallback)
     (1500, 2, 6, 512, 384, True), (700, 4, 16, 256, 512, False), (600, 3, 5, 384, 256, False)])
