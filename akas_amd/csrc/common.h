@@ -64,22 +64,27 @@ AKAS_DEV float e4m3_decode(uint32_t b) {
 // correctly rounded quotient RN(x/s) for finite, non-underflowing operands
 // (Markstein's correction theorem; Muller et al., Handbook of Floating-Point
 // Arithmetic, ch. 4).  Zero keeps x's sign because callers take the sign bit
-// from x, never from q.
+// from x, never from q.  A group holding +-inf has s = inf and r = 0; the
+// correction then runs with 0 in place of s, so every finite x gives
+// q = 0 = RN(x / inf) (with s itself, 0 * inf would make it NaN), and an
+// infinite x gives NaN, as inf / inf does.
 struct GroupScale {
   float s;  // the group scale max(max|x|, 1e-12) / 448
   float r;  // RN(1 / s)
+  float c;  // s in the correction step: s when finite, else 0
 };
 
 AKAS_DEV GroupScale make_group_scale(float amax) {
   GroupScale g;
   g.s = __fdiv_rn(__builtin_fmaxf(amax, 1e-12f), 448.0f);
   g.r = __fdiv_rn(1.0f, g.s);
+  g.c = g.s < __builtin_inff() ? g.s : 0.0f;
   return g;
 }
 
 AKAS_DEV float exact_quotient_magnitude(float ax, const GroupScale& g) {
   float q0 = ax * g.r;
-  float e = __builtin_fmaf(-q0, g.s, ax);
+  float e = __builtin_fmaf(-q0, g.c, ax);
   return __builtin_fmaf(e, g.r, q0);
 }
 

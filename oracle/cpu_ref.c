@@ -275,9 +275,10 @@ int ref_moe_layer_bf16(const uint16_t* x, const float* logits, const uint8_t* w1
 /*
  * Check of the device quotient technique (test infrastructure): for n seeded
  * (x, group max) pairs, compare enc(RN(x/s)) with the device formulation
- * r = RN(1/s), q0 = RN(x*r), e = fma(-q0, s, x), q = fma(e, r, q0) (libm
- * fmaf is correctly rounded).  Returns the number of code mismatches; also
- * counts quotient mismatches into *quotient_mismatch.
+ * r = RN(1/s), q0 = RN(x*r), e = fma(-q0, c, x), q = fma(e, r, q0) with
+ * c = s, or 0 where s is inf (a group holding inf, where x / s = 0 for every
+ * finite x); libm fmaf is correctly rounded.  Returns the number of code
+ * mismatches; also counts quotient mismatches into *quotient_mismatch.
  */
 static uint64_t splitmix(uint64_t* s) {
   uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
@@ -299,11 +300,14 @@ int64_t ref_check_exact_quotient(int64_t n, uint64_t seed, int64_t* quotient_mis
     float x = (float)(((b >> 40) & 1) ? -1 : 1) * amax * frac;
     x = bf16_to_f32(f32_to_bf16(x));
     if (fabsf(x) > amax) x = copysignf(amax, x);
+    /* one sample in 64 as a finite x in a group whose maximum is inf */
+    if (((a >> 58) & 63) == 0) amax = INFINITY;
     float s = fmaxf(amax, 1e-12f) / 448.0f;
     float r = 1.0f / s;
+    float c = isinf(s) ? 0.0f : s;
     float ax = fabsf(x);
     float q0 = ax * r;
-    float e = fmaf(-q0, s, ax);
+    float e = fmaf(-q0, c, ax);
     float q = fmaf(e, r, q0);
     float exact = ax / s;
     if (q != exact) ++qbad;

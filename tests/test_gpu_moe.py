@@ -457,6 +457,57 @@ def test_fused_swiglu_matches_separate_chain_bitwise(dev, rows, top, experts, o,
     assert rel_fro(got, exp) < 1e-2
 
 
+@pytest.mark.parametrize("rows", [33, 1200])
+def test_fused_swiglu_groups_holding_infinity(dev, rows):
+    """Activations that overflow float16 (rows with large activation scales):
+    the fused re-quantization still equals the separate chain bit for bit,
+    scales inf included, and the finite activations of a group holding inf
+    quantize to +-0 (x / inf under IEEE division).  1200 rows take the
+    256-row DMA tiles' epilogue, 33 rows the 32-row tiles'."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(907)
+    top, experts, o, k = 3, 7, 256, 384
+    ids, active = pattern_routes(rows, top, experts, 1)
+    counts, routes = omoe.quantized_routes(ids, active, experts)
+    x = random_codes(rng, (rows, k))
+    w = random_codes(rng, (experts, o, k))
+    w2 = random_codes(rng, (experts, o, k))
+    xs = rng.uniform(0.0625, 0.25, (rows, k // 128)).astype(np.float32)
+    xs[::2] = 8.0  # products of these rows stay finite in float16, their SwiGLU does not
+    ws = ofp8.bf16_round(rng.uniform(0.0625, 0.25, (experts, o // 128, k // 128)).astype(np.float32))
+    ws2 = ofp8.bf16_round(rng.uniform(0.0625, 0.25, (experts, o // 128, k // 128)).astype(np.float32))
+    H = torch.float16
+    args = [_t(x, dev), _t(xs, dev)]
+    cnt, rts = _t(counts, dev), _t(routes, dev)
+    codes, scales = ops.fp8_expert_swiglu(*args, _t(w, dev), _t(ws, dev), _t(w2, dev), _t(ws2, dev),
+                                          cnt, rts, r=rows, top=top, product_dtype=H,
+                                          activation_dtype=H)
+    gate = ops.expert_partial(*args, _t(w, dev), _t(ws, dev), cnt, rts, r=rows, top=top,
+                              output_dtype=H)
+    up = ops.expert_partial(*args, _t(w2, dev), _t(ws2, dev), cnt, rts, r=rows, top=top,
+                            output_dtype=H)
+    act = ops.swiglu_experts(gate, up, output_dtype=H)
+    ecodes, escales = ops.quantize(act, top=top)
+    live = np.zeros((rows, top), bool)
+    for e in range(experts):
+        for route in routes[e, :counts[e]]:
+            live[route // top, route % top] = True
+    assert np.isfinite(_np(gate)[live]).all() and np.isfinite(_np(up)[live]).all()
+    c, s = _np(codes), _np(scales)
+    np.testing.assert_array_equal(c[live], _np(ecodes)[live])
+    np.testing.assert_array_equal(s[live], _np(escales)[live])
+    a = _np(act)
+    in_inf = np.isinf(a).reshape(rows, top, o // 128, 128).any(-1) & live[..., None]
+    assert in_inf.sum() >= 4
+    assert np.isinf(s[in_inf]).all()
+    spread = np.repeat(in_inf, 128, axis=-1) & np.isfinite(a)
+    assert spread.sum() >= 64
+    assert (c[spread] & 0x7F == 0).all()
+    assert (c[np.isinf(a) & live[..., None]] & 0x7F == 126).all()
+
+
 @pytest.mark.parametrize("rows,top,experts,o,k,pd,ad", SWIGLU_CASES)
 def test_fused_swiglu_exact_products_midpoint_band(dev, rows, top, experts, o, k, pd, ad):
     """Exact-product operands (codes {56,64} with sign, scales 0.125; seed 831):

@@ -69,6 +69,38 @@ def test_quantize_large_other_dtypes(dev, dtype):
     np.testing.assert_array_equal(c, ec)
 
 
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("rows,top", [(5, None), (3, 4), (4099, None)])
+def test_quantize_groups_holding_infinity(dev, dtype, rows, top):
+    """A group holding +-inf gets scale inf (max|x| / 448) and its finite
+    values the codes of x / inf = +-0 (IEEE division, as the reference's
+    ``values[j] / scale``, activations/fp8/cuda.py:37-43); an infinite value
+    divides to NaN, which the encoder saturates to magnitude code 126 (the
+    sign of that NaN is the platform's, so only the magnitude is compared).
+    The other groups of the same rows are unaffected."""
+    rng = np.random.default_rng(23)
+    k = 512
+    x = rng.normal(0, 2, (rows * (top or 1), k)).astype(np.float32)
+    x[0, 3] = np.inf
+    x[1, 130] = -np.inf
+    x[2, 256], x[2, 300] = np.inf, -np.inf
+    x[-1, 384:] = np.inf  # a group of infinities only
+    x[-1, 0] = np.inf
+    if top:
+        x = x.reshape(rows, top, k)
+    c, s, ec, es = _run(x, dtype, dev, top)
+    np.testing.assert_array_equal(s, es)
+    assert np.isinf(s.reshape(-1, k // 128)[[0, 1, 2], [0, 1, 2]]).all()
+    finite = np.isfinite(x)
+    np.testing.assert_array_equal(c[finite], ec[finite])
+    assert (c[~finite] & 0x7F == 126).all()
+    # the finite values of the infinite groups are the signed zero codes
+    grp = np.isinf(np.abs(x.reshape(-1, k // 128, 128)).max(-1))
+    in_inf_group = np.repeat(grp, 128, axis=-1).reshape(x.shape) & finite
+    assert in_inf_group.sum() > 100
+    assert (c[in_inf_group] & 0x7F == 0).all()
+
+
 def test_quantize_midpoints_and_subnormals(dev):
     """Values placed exactly on and one ulp around e4m3 rounding midpoints,
     after scaling, and in the e4m3 subnormal range."""
