@@ -227,10 +227,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
   using Plan = StagePlan<BM, BN, THREADS>;
   constexpr int STAGE = (BM + BN) * 128;
   // The 32-row expert partial (the decode down projection) keeps one LDS
-  // stage: 20.9 KB (128 columns) or 36.9 KB (256) lets four workgroups share
-  // a CU instead of three, 38.6 -> 36.6 us at 64 experts x 1536 -> 2048 with
-  // 128 columns.  The paired gate/up kernel was slower that way (86.8 -> 90.6
-  // us) and keeps two.
+  // stage, so that more workgroups share a CU: four instead of three with
+  // 128 columns (20.9 KB; 38.6 -> 36.6 us at 64 experts x 1536 -> 2048), three
+  // instead of two with 256 (36.9 KB; its registers then allow no more).  The
+  // paired gate/up kernel was slower that way (86.8 -> 90.6 us) and keeps two.
   constexpr int NSTAGE = (!PAIRED && BM == 32) ? 1 : 2;
   __shared__ __attribute__((aligned(16))) uint8_t lds[NSTAGE * STAGE];
   __shared__ __attribute__((aligned(16))) float lds_as[NSTAGE][BM];
