@@ -2,11 +2,14 @@
 
 Each function mirrors one graph call kind of the reference (same name, same
 parameter meaning, same buffer names and output order) and calls the gfx950
-C ABI of ``include/akas_fp8.h`` on the current HIP stream.  Outputs may be
+C ABI of ``include/akas_fp8.h`` on the current HIP stream of its tensors'
+device (made current for the call when it is not).  Outputs may be
 passed in (caller-owned buffers, as in the reference runtime) or are
 allocated here with torch.  Invalid geometry raises ``ValueError`` before any
 launch, like the reference factories.  There is no CPU fallback.
 """
+
+import functools
 
 import torch
 
@@ -41,7 +44,28 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
-def _need(t, name, dtype=None, shape=None, device=None):
+def _on_tensor_device(fn):
+    """Run an op on the device of its tensor arguments.  The library launches
+    on the current device and its current stream, so that device is made
+    current for the call when it is not already; device tensors on two
+    different devices raise ``ValueError``."""
+    @functools.wraps(fn)
+    def call(*args, **kwargs):
+        dev = None
+        for a in (*args, *kwargs.values()):
+            if isinstance(a, torch.Tensor) and a.is_cuda:
+                if dev is None:
+                    dev = a.device
+                elif a.device != dev:
+                    raise ValueError(f"{fn.__name__}: tensors on {dev} and {a.device}")
+        if dev is None or dev.index == torch.cuda.current_device():
+            return fn(*args, **kwargs)
+        with torch.cuda.device(dev):
+            return fn(*args, **kwargs)
+    return call
+
+
+def _need(t, name, dtype=None, shape=None):
     if t is None:
         raise ValueError(f"{name} is required")
     if not t.is_cuda:
@@ -76,6 +100,7 @@ _SCALES = (torch.float32, torch.bfloat16)
 # activation / weight codecs
 # ---------------------------------------------------------------------------
 
+@_on_tensor_device
 def quantize(x, *, top=None, out=None, scales=None):
     """``quantize(r, k[, top, input_dtype]): x -> out, scales``.
 
@@ -97,6 +122,7 @@ def quantize(x, *, top=None, out=None, scales=None):
     return out, scales
 
 
+@_on_tensor_device
 def rms_quantize(x, weight, *, eps, zero_centered=False, normalized_dtype=torch.bfloat16,
                  return_normalized=True, normalized=None, out=None, scales=None):
     """RMSNorm fused with ``quantize``: ``x [r, c]`` (f32/f16/bf16), ``weight [c]``
@@ -131,6 +157,7 @@ def rms_quantize(x, weight, *, eps, zero_centered=False, normalized_dtype=torch.
     return (out, scales, y) if return_normalized else (out, scales)
 
 
+@_on_tensor_device
 def dequantize_fp8(codes, scales, *, out=None, out_dtype=None):
     """``dequantize_fp8``: ``decode(codes) * scale`` per 128-group."""
     _need(codes, "codes", torch.uint8)
@@ -142,6 +169,7 @@ def dequantize_fp8(codes, scales, *, out=None, out_dtype=None):
     return out
 
 
+@_on_tensor_device
 def quantize_weight_blocks(w, *, scale_dtype=torch.float32):
     """Block-quantize f32 weights ``[(E,) n, k]`` to e4m3 codes and 128x128 scales.
 
@@ -193,6 +221,7 @@ def linear_workspace(r, k, o, device, stream=None):
     return ws
 
 
+@_on_tensor_device
 def fp8_linear(x, w, scales, *, out=None, out_dtype=None, workspace=None):
     """``fp8_linear(r, k, o[, input_dtype]): x, w, scales -> out``.
 
@@ -219,6 +248,7 @@ def fp8_linear(x, w, scales, *, out=None, out_dtype=None, workspace=None):
     return out
 
 
+@_on_tensor_device
 def fp8_linear_noalloc(x, w, scales, *, out=None, out_dtype=None):
     """:func:`fp8_linear` on the library's static device scratch
     (``akas_fp8_linear_noalloc``): no workspace argument and no device
@@ -241,6 +271,7 @@ def fp8_linear_noalloc(x, w, scales, *, out=None, out_dtype=None):
     return out
 
 
+@_on_tensor_device
 def projection_partial(x, activation_scales, w, scales, *, partitions=1, out=None,
                        out_dtype=None):
     """``projection_partial(r, k, o, partitions)`` on prequantized codes.
@@ -265,6 +296,7 @@ def projection_partial(x, activation_scales, w, scales, *, partitions=1, out=Non
     return out
 
 
+@_on_tensor_device
 def projection_merge(partial, *, out=None, out_dtype=None):
     """``projection_merge(r, o, partitions)``: serial f32 sum over partitions."""
     _need(partial, "partial", torch.float32)
@@ -276,6 +308,7 @@ def projection_merge(partial, *, out=None, out_dtype=None):
     return out
 
 
+@_on_tensor_device
 def expert_merge(partial, *, out=None, output_dtype=None):
     """``expert_merge(r, top, o, partitions)``: ``[r, top, parts, o] -> [r, top, o]``."""
     if partial.dim() != 4:
@@ -287,6 +320,7 @@ def expert_merge(partial, *, out=None, output_dtype=None):
 # routing
 # ---------------------------------------------------------------------------
 
+@_on_tensor_device
 def biased_router(logits, bias, *, top, scale=1.0, normalize=True, ids=None, weights=None):
     """``biased_router(r, experts, top, scale, normalize): logits, bias -> ids, weights``.
 
@@ -304,6 +338,7 @@ def biased_router(logits, bias, *, top, scale=1.0, normalize=True, ids=None, wei
     return ids, weights
 
 
+@_on_tensor_device
 def biased_softmax_router(logits, bias, *, top, scale=1.0, ids=None, weights=None):
     """``biased_softmax_router(r, experts, top, scale)`` (src/akas/ops/moe/kernel.py:444-499)."""
     _need(logits, "logits", torch.float32)
@@ -318,6 +353,7 @@ def biased_softmax_router(logits, bias, *, top, scale=1.0, ids=None, weights=Non
     return ids, weights
 
 
+@_on_tensor_device
 def router(logits, *, top, ids=None, weights=None):
     """``router(r, experts, top): logits -> ids, weights``, the block-fp8
     decode variant's router: selection on the bf16-rounded f32 logits, softmax
@@ -331,6 +367,7 @@ def router(logits, *, top, ids=None, weights=None):
     return ids, weights
 
 
+@_on_tensor_device
 def router_quantize(logits, bias, x, *, top, softmax=True, scale=1.0, normalize=True):
     """The MoE block's router (``biased_softmax_router`` when ``softmax``,
     else ``biased_router``) and ``quantize(x)`` in one launch; up to 64
@@ -355,6 +392,7 @@ def router_quantize(logits, bias, x, *, top, softmax=True, scale=1.0, normalize=
     return ids, weights, codes, scales
 
 
+@_on_tensor_device
 def moe_groups(ids, *, experts=None, routes=None):
     """``moe_groups(r, top): ids -> experts, routes``, the block-fp8 decode
     variant's route tables (src/akas/ops/moe/cuda.py:1978-2008): per (row,
@@ -369,6 +407,7 @@ def moe_groups(ids, *, experts=None, routes=None):
     return experts, routes
 
 
+@_on_tensor_device
 def quantized_routes(ids, active, *, experts, counts=None, routes=None):
     """``quantized_routes(r, experts, top): ids, active -> counts, routes``.
 
@@ -404,6 +443,7 @@ def map_capacity(rows, top, experts):
     return (rows * top + 3) // 4 + experts
 
 
+@_on_tensor_device
 def expert_tile_map(counts, *, r, top, max_block_m=64, tile_experts=None, tile_rows=None):
     """``expert_tile_map(r, experts, top[, max_block_m]): counts -> tile_experts, tile_rows``.
 
@@ -420,6 +460,7 @@ def expert_tile_map(counts, *, r, top, max_block_m=64, tile_experts=None, tile_r
     return tile_experts, tile_rows
 
 
+@_on_tensor_device
 def expert_pack(x, activation_scales, counts, routes, tile_experts, tile_offsets, *, top,
                 max_block_m=64, routed_input=False, packed=None, packed_scales=None,
                 expert_offsets=None):
@@ -454,6 +495,7 @@ def expert_pack(x, activation_scales, counts, routes, tile_experts, tile_offsets
 # grouped expert products
 # ---------------------------------------------------------------------------
 
+@_on_tensor_device
 def expert_partial(x, activation_scales, w, scales, counts, routes, tile_experts=None,
                    tile_offsets=None, expert_offsets=None, *, r, top, routed_input=False,
                    partitions=1, output_dtype=torch.float32, max_block_m=64,
@@ -510,6 +552,7 @@ def combine_arrivals(r, o, device, stream=None):
     return buf
 
 
+@_on_tensor_device
 def expert_combine(x, activation_scales, w, scales, counts, routes, ids, weights, active=None,
                    expert_offsets=None, *, r, top, routed_input=False, packed_input=False,
                    contribution_dtype=torch.float32, max_block_m=64, contributions=None,
@@ -566,6 +609,7 @@ def fp8_experts_workspace(r, top, experts, k, routed_input, device):
     return torch.empty(max(int(n), 1), dtype=torch.uint8, device=device)
 
 
+@_on_tensor_device
 def fp8_experts(x, w, scales, experts, routes, *, top, routed_input=False, out=None,
                 output_dtype=torch.float32, workspace=None):
     """``fp8_experts(r, experts, top, o, k, routed_input)``: the block-fp8
@@ -602,6 +646,7 @@ def fp8_experts(x, w, scales, experts, routes, *, top, routed_input=False, out=N
     return out
 
 
+@_on_tensor_device
 def fp8_expert_swiglu(x, activation_scales, w, scales, w2, scales2, counts, routes,
                       tile_experts=None, tile_offsets=None, expert_offsets=None, *, r, top,
                       product_dtype=torch.float32, activation_dtype=torch.float32,
@@ -661,6 +706,7 @@ def _paired_inputs(x, activation_scales, w, scales, w2, scales2, counts, routes,
     return experts, o, k
 
 
+@_on_tensor_device
 def expert_swiglu(x, activation_scales, w, scales, w2, scales2, counts, routes,
                   tile_experts=None, tile_offsets=None, expert_offsets=None, *, r, top,
                   product_dtype=torch.float32, activation_dtype=torch.float32,
@@ -688,6 +734,7 @@ def expert_swiglu(x, activation_scales, w, scales, w2, scales2, counts, routes,
     return out
 
 
+@_on_tensor_device
 def expert_pair_partial(x, activation_scales, w, scales, w2, scales2, counts, routes,
                         tile_experts=None, tile_offsets=None, *, r, top, partitions=1,
                         max_block_m=64, gate=None, up=None):
@@ -713,6 +760,7 @@ def expert_pair_partial(x, activation_scales, w, scales, w2, scales2, counts, ro
     return gate, up
 
 
+@_on_tensor_device
 def swiglu_experts(g, u, *, round_inputs=False, round_dtype=torch.float32,
                    output_dtype=torch.float32, out=None):
     """``swiglu_experts``: ``g / (1 + exp(-g)) * u`` on ``[r, top, (parts,) c]``.
@@ -734,6 +782,7 @@ def swiglu_experts(g, u, *, round_inputs=False, round_dtype=torch.float32,
     return out
 
 
+@_on_tensor_device
 def moe_combine(experts, weights, shared, gate, *, out=None):
     """``moe_combine(r, top, c): experts, weights, shared, gate -> out``: the
     weighted top-k combine plus a sigmoid-gated shared expert,
@@ -760,6 +809,7 @@ def moe_combine(experts, weights, shared, gate, *, out=None):
     return out
 
 
+@_on_tensor_device
 def routed_combine(experts, weights, active, *, out=None):
     """``routed_combine(r, top, c[, input_dtype]): experts, weights, active -> out``.
 
