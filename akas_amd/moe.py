@@ -263,6 +263,7 @@ def shared_expert_moe(x, logits, shared_gate, weights: ExpertWeights, shared: Sh
     side = _side_stream(x.device)
     width = shared.w1.shape[0]
     side.wait_stream(main)
+    x.record_stream(side)  # read on the side stream: not reused before that work ends
     with torch.cuda.stream(side):  # fp8_linear takes the side stream's own workspace
         g = ops.fp8_linear(x, shared.w1, shared.s1)
         u = ops.fp8_linear(x, shared.w3, shared.s3)
