@@ -847,8 +847,9 @@ static int split_nt(const DenseArgs& a) {
 
 static bool split_fits(const DenseArgs& a) {
   const int esz = a.out_dtype == AKAS_DTYPE_F32 ? 4 : 2;
+  // 32-bit buffer offsets: the fragment-major codes hold M rounded up to 16 rows
   return a.kb_per_part == kSplitQuarters * kSplitKbw && split_nt(a) > 0 &&
-         (int64_t)a.M * a.K < (1ll << 31) && (a.K / kBlock) % 4 == 0 && a.ldo % 4 == 0 &&
+         (int64_t)((a.M + 15) & ~15) * a.K < (1ll << 31) && (a.K / kBlock) % 4 == 0 && a.ldo % 4 == 0 &&
          a.part_stride % 4 == 0 && reinterpret_cast<uintptr_t>(a.out) % (4 * esz) == 0 &&
          reinterpret_cast<uintptr_t>(a.as) % 16 == 0;
 }
