@@ -10,7 +10,8 @@ reference repository root, ``src/akas/...`` or ``tests/...``).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import, call, link or execute anything in this directory, and
-there only as the checker or the timed CPU baseline.  The product path
+there only as the reference the results are compared with, or as the timed
+CPU baseline.  The product path
 (``akas_amd``) never imports it and has no CPU fallback.
 
 Pinning (what each function is checked against, in ``tests/test_oracle_*.py``):
