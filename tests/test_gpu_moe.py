@@ -41,7 +41,7 @@ def pattern_routes(rows, top, experts, mult=1, inactive_last=True):
 
 @pytest.mark.parametrize("rows,experts,top", [(1, 64, 4), (257, 64, 4), (64, 256, 8), (9, 7, 3),
                                               (1000, 64, 8), (33, 32, 6), (17, 64, 1),
-                                              (20, 1000, 6)])
+                                              (20, 1000, 6), (5, 1024, 32), (7, 64, 9)])
 def test_softmax_router(dev, rows, experts, top):
     """Up to 64 experts and top 8 take the sixteen-lanes-per-row kernel, the
     rest the one-wave-per-row kernel (4 expert slots per lane up to 256
@@ -64,7 +64,7 @@ def test_softmax_router(dev, rows, experts, top):
 
 
 @pytest.mark.parametrize("rows,experts,top", [(64, 256, 8), (257, 64, 4), (3, 300, 5), (9, 7, 3),
-                                              (1, 64, 8)])
+                                              (1, 64, 8), (5, 1024, 32)])
 def test_decode_router(dev, rows, experts, top):
     """The block-fp8 router kind: selection on the bf16-rounded logits.  Row 0
     holds 1 and 1 + 2^-10 (one bf16 value) as its two largest logits, the
@@ -86,11 +86,12 @@ def test_decode_router(dev, rows, experts, top):
 
 
 @pytest.mark.parametrize("normalize", [True, False])
-def test_sigmoid_router(dev, normalize):
+@pytest.mark.parametrize("rows,experts,top", [(65, 64, 4), (33, 256, 8), (5, 1024, 32), (9, 7, 3)])
+def test_sigmoid_router(dev, normalize, rows, experts, top):
+    """The sigmoid + bias router up to its limits (1024 experts, top 32)."""
     from akas_amd import ops
 
-    rng = np.random.default_rng(18)
-    rows, experts, top = 65, 64, 4
+    rng = np.random.default_rng(18 + experts)
     logits = rng.normal(0, 1, (rows, experts)).astype(np.float32)
     logits[0] = 0  # exact ties: bias decides, then the lowest id
     bias = (np.arange(experts)[::-1] % 3 * 0.1).astype(np.float32)
