@@ -194,7 +194,8 @@ def test_sigmoid_router_near_ties(dev):
 
 @pytest.mark.parametrize("rows,top,experts,mult", [(1, 4, 64, 1), (33, 2, 4, 1), (1025, 4, 64, 3),
                                                    (16384, 4, 64, 7), (257, 3, 7, 1),
-                                                   (4100, 4, 64, 5), (12, 4, 5, 1)])
+                                                   (4100, 4, 64, 5), (12, 4, 5, 1),
+                                                   (300, 8, 1024, 7), (64, 32, 256, 3)])
 def test_quantized_routes_patterns(dev, rows, top, experts, mult):
     from akas_amd import ops
 
@@ -337,7 +338,9 @@ def _expert_case(rng, rows, top, experts, o, k, routed, exact=True, mult=1):
     (200, 4, 32, 768, 256, True),
     # >= 128 rows per expert: 256-row DMA tiles (ragged last tiles, gathered
     # and routed rows, N = 256 and 512, and N = 384 on the 128-row fallback)
-    (1500, 2, 6, 512, 384, True), (700, 4, 16, 256, 512, False), (600, 3, 5, 384, 256, False)])
+    (1500, 2, 6, 512, 384, True), (700, 4, 16, 256, 512, False), (600, 3, 5, 384, 256, False),
+    # the most experts the entry points take (tile lookup over 16 count chunks)
+    (300, 8, 1024, 128, 256, False)])
 def test_expert_partial_exact(dev, rows, top, experts, o, k, routed):
     import torch
     from akas_amd import ops
