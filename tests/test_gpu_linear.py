@@ -264,6 +264,28 @@ def test_projection_exact_products_dma(dev, m, k, n):
         np.testing.assert_array_equal(out.float().cpu().numpy(), ofp8.round_to(exp, odt))
 
 
+def test_projection_dma_deepest_k(dev):
+    """The prefill kernel at the deepest k range it takes (K = 16384: 128
+    k-blocks, a full weight-scale table) on a ragged 4000 x 3840 output (240
+    tiles).  Scales 2^-2 or 2^-1 keep every partial sum exact in float32 while
+    a wrong k-block or scale index still changes the result; rows from every
+    row tile (the ragged last one included) are compared bit for bit."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(16384)
+    m, k, n = 4000, 16384, 3840
+    x = exact_codes(rng, (m, k))
+    w = exact_codes(rng, (n, k))
+    xs = (2.0 ** rng.integers(-2, 0, (m, k // 128))).astype(np.float32)
+    ws = (2.0 ** rng.integers(-2, 0, (n // 128, k // 128))).astype(np.float32)
+    out = ops.projection_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev))
+    torch.cuda.synchronize()
+    rows = np.array([0, 1, 255, 256, 1023, 2049, 3839, 3840, 3999])
+    exp = ofp8.fp8_linear(x[rows], w, ws, activation_scales=xs[rows])
+    np.testing.assert_array_equal(out.cpu().numpy()[rows], exp)
+
+
 def test_projection_dma_partitions(dev):
     """K-partitions on the prefill kernel (2 x 128 tiles >= 240 workgroups):
     each partition's f32 partial lands at its own offset, bit-exact."""
