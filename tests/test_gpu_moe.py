@@ -355,6 +355,27 @@ def test_expert_partial_exact(dev, rows, top, experts, o, k, routed):
         np.testing.assert_array_equal(_np(out), exp)
 
 
+def test_expert_partial_dma_deepest_k(dev):
+    """The expert prefill kernel (256-row tiles) at the deepest k range it
+    takes: K = 16384, a full 128-entry weight-scale table.  Scales 2^-2 or
+    2^-1 keep every partial sum exact in float32 while a wrong k-block or
+    scale index still changes the result; the whole output is compared."""
+    from akas_amd import ops
+
+    rng = np.random.default_rng(16385)
+    rows, top, experts, o, k = 600, 1, 2, 256, 16384
+    ids, active = pattern_routes(rows, top, experts, 1)
+    counts, routes = omoe.quantized_routes(ids, active, experts)
+    x = exact_codes(rng, (rows, k))
+    w = exact_codes(rng, (experts, o, k))
+    xs = (2.0 ** rng.integers(-2, 0, (rows, k // 128))).astype(np.float32)
+    ws = (2.0 ** rng.integers(-2, 0, (experts, o // 128, k // 128))).astype(np.float32)
+    out = ops.expert_partial(_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev), _t(counts, dev),
+                             _t(routes, dev), r=rows, top=top)
+    exp = omoe.expert_partial(x, xs, w, ws, counts, routes, top)
+    np.testing.assert_array_equal(_np(out), exp)
+
+
 @pytest.mark.parametrize("rows", [257, 1200])
 @pytest.mark.parametrize("out_dtype", ["float32", "bfloat16", "float16"])
 @pytest.mark.parametrize("scale_dtype", ["float32", "bfloat16"])
