@@ -898,10 +898,7 @@ static void launch_dma(const DenseArgs& a, int parts, hipStream_t s) {
   dense_dma_kernel<OUT><<<dim3(tiles, parts), dma::THREADS, 0, s>>>(a);
 }
 
-// Kernel choice by shape: the direct-load small-M kernel up to 64 rows;
-// beyond that the DMA-fed 256x256 kernel when its tiles fill the GPU, else
-// LDS-tiled 256x128 / 128x128 tiles.  Tiled kernels need N to be a multiple of their BN (B rows are
-// addressed affinely); other N fall back to 64-row slices of the small kernel.
+// The direct-load small-M kernel (up to 64 rows) by its row count.
 template <int OUT, int SDT>
 static void launch_small(const DenseArgs& a, int parts, hipStream_t s) {
   if (a.M <= 16)
@@ -979,10 +976,15 @@ static bool launch_wide_m16(const DenseArgs& a, int parts, hipStream_t s) {
   }
 }
 
-// Kernel choice by shape (measured on MI355X, K = 2048, N = 6144):
-//   M <= 64   wide kernel (activations staged once per workgroup in LDS)
-//   M <= 256  64x64 tiles, 2 k-blocks of prefetch
-//   larger    256x128 tiles when they fill the GPU, else 128x128
+// Kernel choice by shape, in order:
+//   16 < M <= 256 with 2048-deep partitions   the split kernel
+//   M <= 64                                   the wide kernel (activations
+//                                             staged once per workgroup in LDS),
+//                                             else the direct small kernel
+//   M > 256 whose 256x256 tiles fill the GPU  the DMA-fed prefill kernel
+//   otherwise                                 64x64 tiles up to 256 rows, then
+//                                             256x128 tiles when they fill the
+//                                             GPU, else 128x128
 // Tiled kernels need N to be a multiple of BN (affine B rows); shapes that
 // fit none of these fall back to 64-row slices of the direct small kernel.
 template <int OUT, int SDT>
