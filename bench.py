@@ -22,7 +22,8 @@ and ``cpu_baseline`` (the oracle's C restatement on the host cores, per
 config).
 
     python bench.py [--steps K] [--warmup W] [--no-extras] [--no-cpu]
-    python bench.py --kernel-probe {decode,prefill,moe_decode,moe_prefill,copy}
+    python bench.py --kernel-probe {decode,decode_m1,decode_m4,decode_m16,decode_m64,
+                                    prefill,moe_decode,moe_prefill,copy}
                                   # launches for rocprofv3 --pmc passes
     python bench.py --roofline-probe   # the measured ceilings alone
     python bench.py --handoff-probe    # fences and atomics between workgroups
@@ -488,16 +489,19 @@ def kernel_probe(torch, dev, what):
     from akas_amd import moe, ops
 
     info = dict(probe=what, copy_bytes=PROBE_COPY_BYTES)
-    if what == "decode":
+    if what == "decode" or what.startswith("decode_m"):
+        m = PROBE_M if what == "decode" else int(what[len("decode_m"):])
+        if m not in DECODE_M:
+            raise SystemExit(f"decode probe rows must be one of {DECODE_M}")
         copies = 20
         codes, scales = make_weights(torch, N_DEC, K_DEC, copies, 1234, dev)
-        x = bf16_activations(torch, PROBE_M, K_DEC, PROBE_M, dev)
-        out = torch.empty((PROBE_M, N_DEC), dtype=torch.bfloat16, device=dev)
-        ws = ops.linear_workspace(PROBE_M, K_DEC, N_DEC, dev)
+        x = bf16_activations(torch, m, K_DEC, m, dev)
+        out = torch.empty((m, N_DEC), dtype=torch.bfloat16, device=dev)
+        ws = ops.linear_workspace(m, K_DEC, N_DEC, dev)
         for i in range(copies):
             ops.fp8_linear(x, codes[i], scales[i], out=out, workspace=ws)
-        info.update(op="fp8_linear M=256 K=2048 N=6144 bf16, x20 on 20 weight copies",
-                    op_bytes=dense_bytes(PROBE_M, K_DEC, N_DEC))
+        info.update(op=f"fp8_linear M={m} K={K_DEC} N={N_DEC} bf16, x20 on 20 weight copies",
+                    op_bytes=dense_bytes(m, K_DEC, N_DEC))
     elif what == "prefill":
         k, n = PREFILL_SHAPES[0]
         codes, scales = make_weights(torch, n, k, 1, 7 + n, dev)
