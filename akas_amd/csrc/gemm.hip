@@ -627,6 +627,7 @@ template <int MT, int NTW, int KS>
 constexpr size_t wide_lds_bytes(int kbp) {
   const size_t stage = (size_t)kbp * 16 * MT * (128 + 4);
   const size_t red = (size_t)KS * NTW * MT * 64 * 16;
+  if (MT == 1) return ((stage + 15) & ~(size_t)15) + red;  // partials beside the slab
   return stage > red ? stage : red;
 }
 
@@ -778,9 +779,15 @@ __global__ __launch_bounds__(64 * NTW * KS) void dense_wide_kernel(DenseArgs p) 
     }
   }
 
-  // 4. fixed-order sum of the KS partial tiles (LDS slab reused)
-  __syncthreads();
-  float* red = reinterpret_cast<float*>(smem);
+  // 4. fixed-order sum of the KS partial tiles (LDS slab reused when the
+  // partials do not fit beside it)
+  float* red;
+  if constexpr (MT == 1) {
+    red = reinterpret_cast<float*>(smem + (((size_t)kbp * 16 * MT * (128 + 4) + 15) & ~(size_t)15));
+  } else {
+    __syncthreads();
+    red = reinterpret_cast<float*>(smem);
+  }
 #pragma unroll
   for (int i = 0; i < MT; ++i)
     *reinterpret_cast<float4*>(red + (((ks * NTW + nt) * MT + i) * 64 + lane) * 4) =
