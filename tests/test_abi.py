@@ -98,3 +98,39 @@ def test_workspace_size_formula():
     # deeper than 2048 at 17-256 rows: f32 partials of the 2048-deep partitions
     assert lib.akas_fp8_linear_workspace_size(64, 8192, 2048) == 64 * 8192 + 64 * 64 * 4 + 64 * 4 * 2048 * 4
     assert lib.akas_fp8_linear_workspace_size(16, 8192, 2048) == 16 * 8192 + 16 * 64 * 4
+
+
+def test_ops_refuse_tensors_on_two_devices():
+    """The Python kinds run on their tensors' device; device tensors on two
+    different devices raise ValueError before the library is called.  (Stand-in
+    tensors report a device, so this runs without a GPU.)"""
+    import pytest
+    import torch
+
+    from akas_amd import ops
+
+    class OnDevice(torch.Tensor):
+        @staticmethod
+        def __new__(cls, t, index):
+            r = torch.Tensor._make_subclass(cls, t)
+            r._index = index
+            return r
+
+        @property
+        def is_cuda(self):
+            return True
+
+        @property
+        def device(self):
+            return torch.device("cuda", self._index)
+
+    x0 = OnDevice(torch.zeros(2, 128), 0)
+    codes1 = OnDevice(torch.zeros(2, 128, dtype=torch.uint8), 1)
+    w1 = OnDevice(torch.zeros(128, 128, dtype=torch.uint8), 1)
+    s1 = OnDevice(torch.zeros(1, 1), 1)
+    with pytest.raises(ValueError, match="tensors on cuda:0 and cuda:1"):
+        ops.quantize(x0, out=codes1)
+    with pytest.raises(ValueError, match="tensors on cuda:0 and cuda:1"):
+        ops.fp8_linear(x0, w1, s1)
+    with pytest.raises(ValueError, match="tensors on cuda:0 and cuda:1"):
+        ops.routed_combine(x0, s1, None)
