@@ -3,6 +3,7 @@
 #include <atomic>
 #include <mutex>
 
+#include "device_info.h"
 #include "gemm_core.h"
 #include "gemm_dma.h"
 #include "quant_group.h"
@@ -914,27 +915,6 @@ static void launch_small(const DenseArgs& a, int parts, hipStream_t s) {
     dense_small_kernel<2, OUT, SDT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
   else
     dense_small_kernel<4, OUT, SDT><<<dim3(a.N / 16, parts), 256, 0, s>>>(a);
-}
-
-// Host-side state kept per device (the current one when a call launches).
-constexpr int kMaxDevices = 64;
-
-static int current_device() {
-  int dev = -1;
-  return hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices ? dev : -1;
-}
-
-// Compute units of the current device (256 when they cannot be read).
-static int device_cus() {
-  static std::atomic<int> cus[kMaxDevices];
-  const int dev = current_device();
-  if (dev < 0) return 256;
-  int c = cus[dev].load(std::memory_order_relaxed);
-  if (c > 0) return c;
-  if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
-    c = 256;
-  cus[dev].store(c, std::memory_order_relaxed);
-  return c;
 }
 
 // Returns false (the caller takes another kernel) when the tile does not

@@ -17,6 +17,9 @@
 // k-block order with acc = fma(P, as*ws, acc), so the fused gate/up values are
 // bit-identical to two expert_partial calls and the fused codes to
 // expert_partial x2 -> swiglu_experts -> quantize.
+#include <algorithm>
+
+#include "device_info.h"
 #include "gemm_core.h"
 #include "gemm_dma.h"
 #include "quant_group.h"
@@ -216,8 +219,13 @@ AKAS_DEV void combine_tail(const ExpertArgs& p, const int* rows_dst, int* taken,
   }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int MODE, int OUT, int SDT>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(ExpertArgs p) {
+// STAGES: LDS stages (0: one for the 32-row expert partial, two otherwise).
+// The one-stage paired 32-row tile keeps its registers within three waves per
+// SIMD, so that three workgroups share a CU.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int MODE, int OUT, int SDT, int STAGES = 0>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N)
+__attribute__((amdgpu_waves_per_eu((STAGES == 1 && BM == 32 && paired_mode(MODE)) ? 3 : 1)))
+void expert_tiled_kernel(ExpertArgs p) {
   constexpr int THREADS = 64 * WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int MT = WM / 16, NT = WN / 16;
@@ -230,8 +238,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void expert_tiled_kernel(Ex
   // stage, so that more workgroups share a CU: four instead of three with
   // 128 columns (20.9 KB; 38.6 -> 36.6 us at 64 experts x 1536 -> 2048), three
   // instead of two with 256 (36.9 KB; its registers then allow no more).  The
-  // paired gate/up kernel was slower that way (86.8 -> 90.6 us) and keeps two.
-  constexpr int NSTAGE = (!PAIRED && BM == 32) ? 1 : 2;
+  // paired gate/up tile takes one stage (three workgroups per CU) only when
+  // its launch asks for it (launch_paired).
+  constexpr int NSTAGE = STAGES ? STAGES : ((!PAIRED && BM == 32) ? 1 : 2);
   __shared__ __attribute__((aligned(16))) uint8_t lds[NSTAGE * STAGE];
   __shared__ __attribute__((aligned(16))) float lds_as[NSTAGE][BM];
   __shared__ int rows_src[BM];
@@ -727,15 +736,15 @@ int64_t capacity_tiles(int64_t r, int64_t top, int64_t experts, int64_t bm) {
   return routes < b ? routes : b;
 }
 
-template <int BM, int BN, int WMW, int WNW, int MODE, int OUT>
+template <int BM, int BN, int WMW, int WNW, int MODE, int OUT, int STAGES = 0>
 static void launch_expert(ExpertArgs a, hipStream_t s) {
   a.max_tiles = (int)capacity_tiles(a.r, a.top, a.E, BM);
   a.tiles_n = paired_mode(MODE) ? a.N / (BN / 2) : a.N / BN;
   dim3 grid((unsigned)(a.max_tiles * a.tiles_n), (unsigned)a.parts);
   if (a.ws_dtype == AKAS_DTYPE_F32)
-    expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_F32><<<grid, 64 * WMW * WNW, 0, s>>>(a);
+    expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_F32, STAGES><<<grid, 64 * WMW * WNW, 0, s>>>(a);
   else
-    expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_BF16><<<grid, 64 * WMW * WNW, 0, s>>>(a);
+    expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_BF16, STAGES><<<grid, 64 * WMW * WNW, 0, s>>>(a);
 }
 
 template <int MODE, int OUT>
@@ -777,7 +786,16 @@ template <int MODE, int OUT>
 static void launch_paired(const ExpertArgs& a, hipStream_t s) {
   const int64_t mean = (int64_t)a.r * a.top / a.E;
   const bool aligned = MODE != kPairPartial || reinterpret_cast<uintptr_t>(a.out2) % 16 == 0;
-  if (mean <= 48)
+  // Decode batches: about one 32-row tile per active expert, at most
+  // min(E, r*top) of them per column block.  When all of those workgroups fit
+  // on the GPU at three per CU, the one-stage tile that allows three runs them
+  // in a single round (LFM2 decode layer, 768 workgroups on 256 CUs: 142.9 ->
+  // 135.5 us); when they do not, the two-stage tile's faster workgroups win
+  // (Qwen3.5 block, about 900 workgroups: 184.0 against 191.4 us one-stage).
+  const int64_t decode_tiles = std::min<int64_t>(a.E, (int64_t)a.r * a.top) * (a.N / 128) * a.parts;
+  if (mean <= 48 && decode_tiles <= 3 * (int64_t)device_cus())
+    launch_expert<32, 256, 1, 4, MODE, OUT, 1>(a, s);
+  else if (mean <= 48)
     launch_expert<32, 256, 1, 4, MODE, OUT>(a, s);
   else if (aligned && expert_dma_fits(a, mean, dma::BN / 2))
     launch_expert_dma<MODE, OUT>(a, s);
