@@ -931,8 +931,12 @@ static bool launch_wide(const DenseArgs& a, int parts, hipStream_t s) {
   if (dev < 0) return false;
   if (!((configured.load(std::memory_order_acquire) >> dev) & 1u)) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
+      // The caller launches another kernel instead; the failed call must not
+      // leave its error for the launch check after that kernel.
+      (void)hipGetLastError();
       return false;
+    }
     configured.fetch_or(uint64_t{1} << dev, std::memory_order_release);
   }
   kern<<<dim3(a.N / CW, parts), 64 * NTW * KS, lds, s>>>(a);

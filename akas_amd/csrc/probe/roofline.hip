@@ -6,12 +6,7 @@
 //                  stored only if it matches a sentinel (so the loads stay but
 //                  nothing is written);
 //   mfma        -- back-to-back FP8 MFMAs (16x16x128, OCP e4m3 operands in
-//                  registers) on four independent accumulators per wave;
-//   handoff     -- what a hand-off between workgroups inside one launch
-//                  costs: each workgroup writes its block of data, then
-//                  (by mode) a device-scope release fence, one relaxed
-//                  device-scope atomic add on a shared counter, a device-scope
-//                  acquire fence, and a read of its neighbour's block.
+//                  registers) on four independent accumulators per wave.
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -89,36 +84,6 @@ PROBE_API int akas_probe_stream_read(const void* src, size_t bytes, uint32_t* si
 PROBE_API int akas_probe_mfma(uint32_t* sink, int iters, int blocks, void* stream) {
   if (!sink || iters < 1 || blocks < 1) return -1;
   mfma_kernel<<<blocks, kThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(sink, iters);
-  return hipGetLastError() == hipSuccess ? 0 : -4;
-}
-
-// handoff modes (bits): 1 release fence, 2 acquire fence, 4 arrival
-// atomic, 8 read the next workgroup's block after the acquire.
-__global__ __launch_bounds__(kThreads) void handoff_kernel(uint32_t* __restrict__ data,
-                                                           uint32_t* __restrict__ counter, int words,
-                                                           int mode) {
-  uint32_t* mine = data + (size_t)blockIdx.x * words;
-  for (int i = threadIdx.x; i < words; i += kThreads) mine[i] = (uint32_t)i ^ blockIdx.x;
-  if (mode & 1) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (threadIdx.x == 0 && (mode & 4))
-    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (mode & 2) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  if (mode & 8) {
-    const uint32_t* other = data + (size_t)((blockIdx.x + 1) % gridDim.x) * words;
-    uint32_t fold = 0;
-    for (int i = threadIdx.x; i < words; i += kThreads) fold += other[i];
-    if (fold == kSentinel) counter[1 + threadIdx.x] = fold;
-  }
-}
-
-// data holds blocks * words dwords, counter 1 + 256 dwords.
-PROBE_API int akas_probe_handoff(void* data, void* counter, int blocks, int words, int mode,
-                                 void* stream) {
-  if (!data || !counter || blocks < 1 || words < 1 || mode < 0 || mode > 15) return -1;
-  handoff_kernel<<<blocks, kThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      reinterpret_cast<uint32_t*>(data), reinterpret_cast<uint32_t*>(counter), words, mode);
   return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

@@ -186,8 +186,12 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
     rows = x.shape[0]
     if partition_maximum_rows is not None and rows > partition_maximum_rows:
         partitions = 1
-    if partitions > 1 and packed:
-        raise ValueError("the partitions policy applies to compact (unpacked) experts")
+    if packed:
+        # The partitions rewrite splits compact expert calls only; packed
+        # calls keep one partition (src/akas/ops/moe/definition.py:796-815),
+        # as the reference's seed combining "partitions: 2" with "packed:
+        # True" runs (:637-652).
+        partitions = 1
     if active is None:
         active = _all_active(rows, x.device)
     quantized = None

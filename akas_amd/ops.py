@@ -9,6 +9,7 @@ allocated here with torch.  Invalid geometry raises ``ValueError`` before any
 launch, like the reference factories.  There is no CPU fallback.
 """
 
+import collections
 import functools
 
 import torch
@@ -194,42 +195,96 @@ def quantize_weight_blocks(w, *, scale_dtype=torch.float32):
 # dense linear
 # ---------------------------------------------------------------------------
 
-_WORKSPACES = {}  # (device index, stream handle) -> workspace of that stream
-_RETIRED = []     # workspaces outgrown by their stream, kept alive for good
+class _StreamBuffers:
+    """Device buffers cached per (device, stream): calls sharing a buffer must
+    be ordered on one stream, so each stream gets its own.
+
+    At most ``LIMIT`` streams per device keep a buffer; the least recently
+    used one is dropped beyond that, and a buffer outgrown by its stream is
+    replaced.  Each buffer is allocated with its own stream current, so
+    dropping it is stream-ordered: torch's caching allocator hands that
+    memory only to later allocations on the same stream.  A buffer that was
+    used while a HIP graph was being captured is retired instead, never
+    freed, since a replay of that graph still addresses it.
+
+    Streams are told apart by their handle.  torch's streams come from pools
+    that are never destroyed; a caller who destroys an external stream must
+    first synchronize it, or a new stream given the same handle would share
+    the buffer with work still in flight.
+    """
+
+    LIMIT = 16
+
+    def __init__(self, make):
+        self._make = make  # (elements, device index) -> new tensor
+        self._entries = collections.OrderedDict()  # key -> [tensor, used under capture]
+
+    def get(self, need, device, stream=None):
+        device = torch.device(device)
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        if stream is None:
+            stream = torch.cuda.current_stream(index)
+        key = (index, stream.cuda_stream)
+        capturing = torch.cuda.is_current_stream_capturing()
+        entry = self._entries.get(key)
+        if entry is not None:
+            self._entries.move_to_end(key)
+            if entry[0].numel() >= need:
+                entry[1] = entry[1] or capturing
+                return entry[0]
+            self._drop(self._entries.pop(key))
+        with torch.cuda.stream(stream):
+            buf = self._make(need, index)
+        self._entries[key] = [buf, capturing]
+        mine = [k for k in self._entries if k[0] == index]
+        for old in mine[:max(0, len(mine) - self.LIMIT)]:
+            self._drop(self._entries.pop(old))
+        return buf
+
+    def __len__(self):
+        return len(self._entries)
+
+    @staticmethod
+    def _drop(entry):
+        if entry[1]:
+            _RETIRED.append(entry[0])
+
+
+_RETIRED = []  # buffers a captured graph may still address, kept for good
+_WORKSPACES = _StreamBuffers(
+    lambda need, index: torch.empty(max(need, 1 << 20), dtype=torch.uint8,
+                                    device=torch.device("cuda", index)))
 
 
 def linear_workspace(r, k, o, device, stream=None):
-    """Cached workspace for :func:`fp8_linear`, one per device and stream.
-
-    Calls sharing a workspace must be ordered on one stream, so each stream
-    gets its own.  When a larger problem outgrows a stream's workspace, the
-    old one is retired but never freed: a HIP graph captured earlier may
-    still hold its address.  The contents need no initialization.
-    """
+    """Cached workspace for :func:`fp8_linear`, one per device and stream
+    (see ``_StreamBuffers``).  The contents need no initialization."""
     need = _lib.load().akas_fp8_linear_workspace_size(r, k, o)
-    device = torch.device(device)
-    index = device.index if device.index is not None else torch.cuda.current_device()
-    if stream is None:
-        stream = torch.cuda.current_stream(index)
-    key = (index, stream.cuda_stream)
-    ws = _WORKSPACES.get(key)
-    if ws is None or ws.numel() < need:
-        if ws is not None:
-            _RETIRED.append(ws)
-        ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", index))
-        _WORKSPACES[key] = ws
-    return ws
+    return _WORKSPACES.get(need, device, stream)
 
 
 @_on_tensor_device
-def fp8_linear(x, w, scales, *, out=None, out_dtype=None, workspace=None):
-    """``fp8_linear(r, k, o[, input_dtype]): x, w, scales -> out``.
+def fp8_linear(x, w, scales, activation_scales=None, *, out=None, out_dtype=None,
+               workspace=None):
+    """``fp8_linear(r, k, o[, input_dtype]): x, w, scales[, activation_scales] -> out``.
 
     ``x`` f32/f16/bf16 ``[r, k]`` is quantized per 1x128 group, multiplied by
     the e4m3 weight ``[o, k]`` with 128x128 block ``scales`` (f32 or bf16,
-    ``[ceil(o/128), k/128]``), f32 accumulation, stored as ``out_dtype``.
-    (src/akas/ops/linear/cuda.py:642-646, :757-828)
+    ``[ceil(o/128), k/128]``), f32 accumulation, stored as ``out_dtype``
+    (src/akas/ops/linear/cuda.py:642-646, :757-828).
+
+    With ``activation_scales`` (f32 ``[r, k/128]``), ``x`` holds e4m3 codes
+    (uint8 ``[r, k]``) already quantized, as the reference binds its block-FP8
+    prefill registration (``fp8_prequantized``,
+    src/akas/ops/linear/definition.py:558-568, :942-963): the product then
+    runs on ``akas_projection_partial`` with one partition and no workspace.
     """
+    if activation_scales is not None:
+        if workspace is not None:
+            raise ValueError("prequantized fp8_linear takes no workspace")
+        _need(x, "x", torch.uint8)
+        return projection_partial(x, activation_scales, w, scales, partitions=1, out=out,
+                                  out_dtype=out_dtype)
     _need(x, "x", _FLOATS)
     _need(w, "w", torch.uint8)
     if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
@@ -530,26 +585,16 @@ def expert_partial(x, activation_scales, w, scales, counts, routes, tile_experts
     return out
 
 
-_ARRIVALS = {}  # (device index, stream handle) -> expert_combine arrival counters
+_ARRIVALS = _StreamBuffers(
+    lambda need, index: torch.zeros(max(need, 1 << 16), dtype=torch.int32,
+                                    device=torch.device("cuda", index)))
 
 
 def combine_arrivals(r, o, device, stream=None):
     """Arrival counters of :func:`expert_combine`, one zeroed buffer per device
-    and stream (every call leaves its counters zero again, so calls ordered
-    on one stream share it).  An outgrown buffer is retired, never freed."""
-    need = r * (o // BLOCK)
-    device = torch.device(device)
-    index = device.index if device.index is not None else torch.cuda.current_device()
-    if stream is None:
-        stream = torch.cuda.current_stream(index)
-    key = (index, stream.cuda_stream)
-    buf = _ARRIVALS.get(key)
-    if buf is None or buf.numel() < need:
-        if buf is not None:
-            _RETIRED.append(buf)
-        buf = torch.zeros(max(need, 1 << 16), dtype=torch.int32, device=torch.device("cuda", index))
-        _ARRIVALS[key] = buf
-    return buf
+    and stream (see ``_StreamBuffers``); every call leaves its counters zero
+    again, so calls ordered on one stream share it."""
+    return _ARRIVALS.get(r * (o // BLOCK), device, stream)
 
 
 @_on_tensor_device

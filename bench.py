@@ -6,16 +6,18 @@ activations ``[M, 2048]`` (~N(0,1), 1% of entries x20) for M in
 block scales; one step = one ``fp8_linear`` (1x128 quantize + block-scaled
 MFMA GEMM, bf16 out) per M.  The value is whole-step algorithmic HBM bytes
 per second, ``sum_M N*K + 4*ceil(N/128)*K/128 + 2*M*K + 2*M*N`` over the
-step time.  Every step reads a different copy of the weights (more than
-512 MB of copies in rotation), so weights stream from HBM, not from the
-256 MB last-level cache.  ``--warmup W`` steps run first, then exactly
-``--steps K`` steps are timed as one replay of a HIP graph holding them.
+step time.  Every op of a step reads its own copy of the weights, from a
+rotation of more than twice the 256 MB last-level cache, which is emptied
+before the timed region, so weights stream from HBM.  ``--warmup W`` steps
+run first, then exactly ``--steps K`` steps are timed as one replay of a HIP
+graph holding them.
 
 Also reported: ``roofline`` for the dominant op of the step (the M=256
 ``fp8_linear``, every launch it makes), ``roofline_prefill`` for the
-prefill GEMM kernel (MFMA-bound), ``ceilings`` measured by the probe library
+prefill ``fp8_linear`` op at M=8192, K=2048, N=6144 (its quantizer and GEMM
+launches; MFMA-bound), ``ceilings`` measured by the probe library
 (streaming HBM read, FP8 MFMA), ``extras`` (the prefill GEMMs, the MoE
-decode layer, the skewed MoE prefill layer, the fused RMSNorm + quantizer
+decode layer unpacked and packed, the skewed MoE prefill layer, the fused RMSNorm + quantizer
 and the shared-expert MoE block; each MoE block timed as one of four
 captured back to back in a graph, as a decode step graph holds many layers)
 and ``cpu_baseline`` (the oracle's C restatement on the host cores, per
@@ -26,7 +28,6 @@ config).
                                     prefill,moe_decode,moe_prefill,copy}
                                   # launches for rocprofv3 --pmc passes
     python bench.py --roofline-probe   # the measured ceilings alone
-    python bench.py --handoff-probe    # fences and atomics between workgroups
 """
 
 import argparse
@@ -151,14 +152,30 @@ def graph_of(torch, fn, n):
     return g
 
 
+LLC_BYTES = 256 << 20  # MI355X last-level cache (MALL)
+
+
+def _evict_llc(torch, dev):
+    """Write 1 GiB (four times the last-level cache) so that no weight copy
+    is cache-resident when a timed region starts."""
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+    torch.cuda.synchronize()
+    del buf
+
+
 def decode_sweep(torch, dev, steps, warmup):
     """The headline: ``warmup`` eager steps, then exactly ``steps`` steps timed
-    as one replay of a graph that holds them (step i on weight copy
-    i % copies), with a barrier (synchronize) on both sides."""
+    as one replay of a graph that holds them, with a barrier (synchronize) on
+    both sides.  Every op reads its own weight copy: op j of step i reads copy
+    (5 i + j) mod ``copies``, and the copies hold more than twice the
+    last-level cache, so no launch reads a copy that the previous
+    ``copies - 1`` launches left in the cache; the cache is emptied before the
+    timed replay, so its first launches read cold copies too."""
     from akas_amd import ops
 
     wbytes = N_DEC * K_DEC
-    copies = max(8, math.ceil(640e6 / wbytes))
+    copies = math.ceil(2 * LLC_BYTES / wbytes) + 1
     codes, scales = make_weights(torch, N_DEC, K_DEC, copies, 1234, dev)
     xs = {m: bf16_activations(torch, m, K_DEC, m, dev) for m in DECODE_M}
     outs = {m: torch.empty((m, N_DEC), dtype=torch.bfloat16, device=dev) for m in DECODE_M}
@@ -166,15 +183,16 @@ def decode_sweep(torch, dev, steps, warmup):
     step_bytes = sum(dense_bytes(m, K_DEC, N_DEC) for m in DECODE_M)
 
     def step(i):
-        c, s = codes[i % copies], scales[i % copies]
-        for m in DECODE_M:
-            ops.fp8_linear(xs[m], c, s, out=outs[m], workspace=ws)
+        for j, m in enumerate(DECODE_M):
+            c = (len(DECODE_M) * i + j) % copies
+            ops.fp8_linear(xs[m], codes[c], scales[c], out=outs[m], workspace=ws)
 
     for i in range(warmup):
         step(i)
     g = graph_of(torch, step, steps)
     g.replay()  # the graph's first replay uploads it; untimed
     torch.cuda.synchronize()
+    _evict_llc(torch, dev)
     t0 = time.perf_counter()
     g.replay()
     torch.cuda.synchronize()
@@ -199,7 +217,8 @@ def decode_sweep(torch, dev, steps, warmup):
                           gemm_us=round(ms * 1e3, 3), gemm_bytes=b,
                           gemm_gbs=round(b / (ms * 1e-3) / 1e9, 1),
                           tflops=round(2 * m * K_DEC * N_DEC / (op_ms * 1e-3) / 1e12, 2)))
-    return dict(step_s=dt, step_bytes=step_bytes, per_m=per_m, copies=copies, steps=steps)
+    return dict(step_s=dt, step_bytes=step_bytes, per_m=per_m, copies=copies, steps=steps,
+                touched=min(copies, len(DECODE_M) * steps))
 
 
 PREFILL_SHAPES = ((2048, 6144), (2048, 8192), (8192, 2048))
@@ -592,37 +611,6 @@ def roofline_ceilings(torch, dev):
                 source="akas_amd/csrc/probe/roofline.hip")
 
 
-HANDOFF_MODES = {"plain": 0, "atomic": 4, "release+atomic": 5, "atomic+acquire": 6,
-                 "release+atomic+acquire": 7, "release+atomic+acquire+read": 15}
-
-
-def handoff_probe(torch, dev):
-    """Cost per launch of a hand-off between workgroups inside one launch
-    (device-scope release / acquire fences and one shared-counter atomic per
-    workgroup), graph-timed over 20 launches, by workgroup count and bytes
-    written per workgroup."""
-    import ctypes
-
-    from akas_amd import build
-
-    lib = ctypes.CDLL(build.PROBE_LIBRARY)
-    lib.akas_probe_handoff.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
-                                       ctypes.c_int, ctypes.c_void_p]
-    data = torch.zeros(1024 * 16384, dtype=torch.int32, device=dev)
-    counter = torch.zeros(257, dtype=torch.int32, device=dev)
-    rows = []
-    for blocks in (8, 64, 256, 1024):
-        for words in (1024, 16384):
-            row = dict(workgroups=blocks, bytes_per_workgroup=4 * words)
-            for name, mode in HANDOFF_MODES.items():
-                us = time_kernel_graph(torch, lambda i: lib.akas_probe_handoff(
-                    data.data_ptr(), counter.data_ptr(), blocks, words, mode,
-                    torch.cuda.current_stream().cuda_stream), 20) * 1e3
-                row[name] = round(us, 2)
-            rows.append(row)
-    return rows
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -634,8 +622,6 @@ def main():
                     help="only launch one workload and a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--roofline-probe", action="store_true",
                     help="only measure the streaming-read and FP8 MFMA ceilings")
-    ap.add_argument("--handoff-probe", action="store_true",
-                    help="only measure the cost of fences and atomics between workgroups")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported "
@@ -657,10 +643,6 @@ def main():
     if args.roofline_probe:
         print(json.dumps(roofline_ceilings(torch, dev)))
         return
-    if args.handoff_probe:
-        for row in handoff_probe(torch, dev):
-            print(json.dumps(row))
-        return
 
     dec = decode_sweep(torch, dev, args.steps, args.warmup)
     value = dec["step_bytes"] / dec["step_s"] / 1e9
@@ -681,22 +663,30 @@ def main():
                 config=dict(workload="decode-shape dense FP8 linear sweep", M=list(DECODE_M),
                             K=K_DEC, N=N_DEC, x="bf16 ~N(0,1), 1% x20", w="e4m3 N(0,0.02), "
                             "128x128 f32 block scales", out="bf16",
-                            weight_copies_rotated=dec["copies"]),
+                            weight_copies_rotated=dec["copies"],
+                            weight_copies_read_in_timed_region=dec["touched"],
+                            weight_copy_bytes=N_DEC * K_DEC),
                 roofline=roofline, sweep=dec["per_m"])
     line["ceilings"] = roofline_ceilings(torch, dev)
     if not args.no_extras:
         prefill = prefill_gemms(torch, dev, 20)
         top = prefill[0]
         busy = profile_value(PREFILL_COUNTERS, "mfma_busy_frac")
+        traffic = profile_value(PREFILL_COUNTERS, "traffic_bytes_per_op")
         line["roofline_prefill"] = dict(
-            bound="mfma", achieved=top["gemm_tflops"], peak=FP8_PEAK_TFLOPS, unit="TFLOP/s",
-            frac=round(top["gemm_tflops"] / FP8_PEAK_TFLOPS, 4), traffic=None,
-            kernel=f"prefill GEMM launch of fp8_linear, M=8192, K={top['K']}, N={top['N']}, bf16 out",
-            flops_per_launch=2 * 8192 * top["K"] * top["N"], avg_us=top["gemm_us"],
-            mfma_busy_frac=busy, counters_source=f"profiles/{PREFILL_COUNTERS}" if busy else None)
+            bound="mfma", achieved=top["op_tflops"], peak=FP8_PEAK_TFLOPS, unit="TFLOP/s",
+            frac=round(top["op_tflops"] / FP8_PEAK_TFLOPS, 4),
+            traffic=int(traffic) if traffic else None,
+            kernel=f"fp8_linear op at M=8192, K={top['K']}, N={top['N']}, bf16 in and out (its "
+                   f"quantizer launch and its GEMM launch)",
+            flops_per_launch=2 * 8192 * top["K"] * top["N"], avg_us=top["op_us"],
+            gemm_launch_us=top["gemm_us"], gemm_launch_frac=top["gemm_frac_fp8"],
+            mfma_busy_frac=busy,
+            counters_source=f"profiles/{PREFILL_COUNTERS}" if busy or traffic else None)
         line["extras"] = dict(
             prefill_gemm=prefill,
             moe_decode=moe_layer_bench(torch, dev, 256, False, 20),
+            moe_decode_packed=moe_layer_bench(torch, dev, 256, False, 20, packed=True),
             moe_prefill_zipf=moe_layer_bench(torch, dev, 16384, True, 10),
             moe_prefill_zipf_packed=moe_layer_bench(torch, dev, 16384, True, 10, packed=True),
             rms_quantize=rms_quantize_bench(torch, dev),

@@ -443,3 +443,62 @@ def test_fp8_linear_default_workspace_per_stream(dev):
     for j in range(len(streams)):
         for i in range(len(xs)):
             np.testing.assert_array_equal(outs[j][i].cpu().numpy(), ref[i].cpu().numpy())
+
+
+@pytest.mark.parametrize("m", [16, 8192])
+def test_fp8_linear_prequantized_binding(dev, m):
+    """``fp8_linear`` bound as the reference's block-FP8 prefill registration
+    binds it (u8 codes ``x`` plus ``activation_scales``,
+    src/akas/ops/linear/definition.py:558-568, :942-963) equals
+    ``projection_partial`` with one partition bit for bit, and the oracle to
+    the GEMM bar."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(101 + m)
+    codes, scales = block_weights(rng, (6144, 2048))
+    w, s = _t(codes, dev), _t(scales, dev)
+    x = bf16_normal(rng, (m, 2048), outliers=0.01)
+    xc, xs = ops.quantize(_t(x, dev, torch.bfloat16))
+    got = ops.fp8_linear(xc, w, s, xs, out_dtype=torch.bfloat16)
+    ref = ops.projection_partial(xc, xs, w, s, partitions=1, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert got.dtype == torch.bfloat16 and tuple(got.shape) == (m, 6144)
+    assert torch.equal(got, ref)
+    rows = slice(0, m) if m <= 256 else np.r_[0:64, m - 64:m]
+    exp = ofp8.fp8_linear(x[rows], codes, scales)
+    assert rel_fro(got.float().cpu().numpy()[rows], exp) < 4e-3
+    # the same kind into a caller-owned f32 output
+    out = torch.empty((m, 6144), dtype=torch.float32, device=dev)
+    ops.fp8_linear(xc, w, s, activation_scales=xs, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ops.projection_partial(xc, xs, w, s, out_dtype=torch.float32))
+    with pytest.raises(ValueError):  # codes must be u8 when scales are bound
+        ops.fp8_linear(_t(x, dev, torch.bfloat16), w, s, xs)
+
+
+def test_linear_workspace_cache_is_bounded(dev):
+    """Calls cycling through more streams than the per-device cache keeps
+    leave at most that many workspaces cached, and every result equals the
+    one-stream result (a dropped workspace is freed in its stream's order)."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(23)
+    codes, scales = block_weights(rng, (2048, 2048))
+    w, s = _t(codes, dev), _t(scales, dev)
+    x = _t(bf16_normal(rng, (64, 2048)), dev, torch.bfloat16)
+    ref = ops.fp8_linear(x, w, s)
+    torch.cuda.synchronize()
+    limit = ops._StreamBuffers.LIMIT
+    streams = [torch.cuda.Stream() for _ in range(limit + 8)]
+    outs = []
+    for rep in range(2):
+        for st in streams:
+            st.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(st):
+                outs.append(ops.fp8_linear(x, w, s))
+    torch.cuda.synchronize()
+    assert sum(1 for key in ops._WORKSPACES._entries if key[0] == dev.index) <= limit
+    for out in outs:
+        assert torch.equal(out, ref)

@@ -990,6 +990,12 @@ def test_routed_moe_layer_partitions_policy(dev, rows, parts):
                          partition_maximum_rows=rows - 1)
     plain = moe.routed_moe(xt, lt, None, wts, top=top)
     np.testing.assert_array_equal(_np(off), _np(plain))
+    # Packed expert calls are not partitioned (the rewrite splits compact
+    # calls only, src/akas/ops/moe/definition.py:796-815): a plan combining
+    # both, as the reference's sm_90a seed does, runs the packed block.
+    packed = moe.routed_moe(xt, lt, None, wts, top=top, partitions=parts, packed=True)
+    np.testing.assert_array_equal(
+        _np(packed), _np(moe.routed_moe(xt, lt, None, wts, top=top, packed=True)))
 
 
 @pytest.mark.parametrize("rows,packed,fused,policy", [
