@@ -28,6 +28,7 @@ config).
                                     prefill,moe_decode,moe_prefill,copy}
                                   # launches for rocprofv3 --pmc passes
     python bench.py --roofline-probe   # the measured ceilings alone
+    python bench.py --operand-probe    # prefill GEMM: random against constant operands
 """
 
 import argparse
@@ -557,6 +558,38 @@ def kernel_probe(torch, dev, what):
     print(json.dumps(info))
 
 
+OPERAND_CODES = {"random": None, "zero": 0x00, "one": 0x38, "max": 0x7E}
+
+
+def operand_probe(torch, dev, rounds=3, launches=10):
+    """The prefill GEMM launch (M=8192, K=2048, N=6144, bf16 out) on random
+    e4m3 operands and on constant ones (every code 0x00, 0x38 = 1.0 or
+    0x7E = 448), interleaved over ``rounds``: identical instructions and
+    addresses, different data.  Each line is TFLOP/s from HIP events around a
+    graph of ``launches`` launches.  Under rocprofv3 --pmc GRBM_GUI_ACTIVE
+    with --kernel-trace, the clock the chip ran at is GRBM_GUI_ACTIVE / 8 XCDs
+    over each dispatch's duration."""
+    from akas_amd import ops
+
+    m, (k, n) = 8192, PREFILL_SHAPES[0]
+    codes, scales = make_weights(torch, n, k, 1, 7 + n, dev)
+    x = bf16_activations(torch, m, k, 99, dev, outliers=0.0)
+    q, qs = ops.quantize(x)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    operands = {}
+    for name, code in OPERAND_CODES.items():
+        operands[name] = ((q, codes[0]) if code is None else
+                          (torch.full_like(q, code), torch.full_like(codes[0], code)))
+    flops = 2 * m * k * n
+    for r in range(rounds):
+        row = dict(round=r)
+        for name, (a, w) in operands.items():
+            ms = time_kernel_graph(torch, lambda i: ops.projection_partial(
+                a, qs, w, scales[0], out=out, out_dtype=torch.bfloat16), launches)
+            row[name] = round(flops / (ms * 1e-3) / 1e12, 1)
+        print(json.dumps(row), flush=True)
+
+
 def roofline_ceilings(torch, dev):
     """The GPU's measured ceilings from the probe library: a streaming read
     of 1 GiB (four times the 256 MB last-level cache) at several grid sizes,
@@ -622,6 +655,8 @@ def main():
                     help="only launch one workload and a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--roofline-probe", action="store_true",
                     help="only measure the streaming-read and FP8 MFMA ceilings")
+    ap.add_argument("--operand-probe", action="store_true",
+                    help="only time the prefill GEMM on random against constant operands")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported "
@@ -642,6 +677,9 @@ def main():
         return
     if args.roofline_probe:
         print(json.dumps(roofline_ceilings(torch, dev)))
+        return
+    if args.operand_probe:
+        operand_probe(torch, dev)
         return
 
     dec = decode_sweep(torch, dev, args.steps, args.warmup)
