@@ -629,6 +629,25 @@ def roofline_ceilings(torch, dev):
             torch.cuda.current_stream().cuda_stream), copies)
         best_op = min(best_op, (ms * 1e3, blocks))
     del wbufs
+    lib.akas_probe_load_mix.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_void_p]
+    # The split GEMM's loads alone (M = 64 and 256), over the same rotation of
+    # weight copies, with row-major (as projection_partial reads them) and
+    # fragment-major (as fp8_linear's quantizer writes them) activations.
+    wbufs = torch.randint(0, 256, (copies, wbytes), dtype=torch.uint8, device=dev)
+    load_mix = {}
+    for m in (64, 256):
+        acts = torch.randint(0, 256, ((m + 15) // 16 * 16 * K_DEC,), dtype=torch.uint8, device=dev)
+        sink = torch.empty(2048 * 512, dtype=torch.int32, device=dev)
+        row = {}
+        for af, key in ((0, "row_major_us"), (1, "fragment_major_us")):
+            ms = time_kernel_graph(torch, lambda i: lib.akas_probe_load_mix(
+                wbufs[i % copies].data_ptr(), acts.data_ptr(), m, N_DEC, af, sink.data_ptr(), None,
+                torch.cuda.current_stream().cuda_stream), copies)
+            row[key] = round(ms * 1e3, 3)
+        load_mix[f"M{m}"] = row
+    del wbufs
     iters, blocks = 4000, 256 * 8
     sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
@@ -641,6 +660,7 @@ def roofline_ceilings(torch, dev):
                 decode_weight_read_us=round(best_op[0], 3), decode_weight_read_grid=best_op[1],
                 decode_weight_read_gbs=round(wbytes / (best_op[0] * 1e-6) / 1e9, 1),
                 decode_step_read_floor_us=round(len(DECODE_M) * best_op[0], 3),
+                split_gemm_loads_alone=load_mix,
                 source="akas_amd/csrc/probe/roofline.hip")
 
 
