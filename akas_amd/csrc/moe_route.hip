@@ -605,7 +605,9 @@ __global__ __launch_bounds__(256) void combine8_kernel(const void* __restrict__ 
   const int64_t col = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
   if (col >= c) return;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (!active || active[row] != 0) {
+  // The contributions' loads are in bounds for every row, so they go out
+  // without waiting for the row's flag, which only selects the result.
+  {
     constexpr int U = 4;
     for (int k0 = 0; k0 < top; k0 += U) {
       u32x4 raw[U][DT == AKAS_DTYPE_F32 ? 2 : 1];
@@ -623,9 +625,13 @@ __global__ __launch_bounds__(256) void combine8_kernel(const void* __restrict__ 
           raw[u][0] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(experts) + base);
         }
       }
+      // Rank by rank, each fold kept or discarded by a select rather than a
+      // branch, so that all of the ranks' loads above go out before the first
+      // fold waits for one (a branch per rank let the compiler sink each load
+      // behind the previous rank's wait).
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        if (k0 + u >= top) break;
+        const bool folds = k0 + u < top;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           float v;
@@ -636,10 +642,15 @@ __global__ __launch_bounds__(256) void combine8_kernel(const void* __restrict__ 
           else
             v = f16_bits_to_f32((raw[u][0][j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
           if constexpr (SHARED && DT != AKAS_DTYPE_BF16) v = round_bf16(v);
-          acc[j] = __builtin_fmaf(v, wv[u], acc[j]);
+          const float f = __builtin_fmaf(v, wv[u], acc[j]);
+          acc[j] = folds ? f : acc[j];
         }
       }
     }
+  }
+  if (active && active[row] == 0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
   }
   if constexpr (SHARED) {
     const float g = round_bf16(load_elem(gate, row, gate_dtype));
