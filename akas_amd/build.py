@@ -40,13 +40,13 @@ FLAGS = [
 ]
 
 
-def sources():
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+def sources(csrc=CSRC):
+    return sorted(os.path.join(csrc, f) for f in os.listdir(csrc) if f.endswith(".hip"))
 
 
-def _compile(src):
+def _compile(src, objdir=OBJDIR):
     sub = "probe_" if os.path.dirname(src) == PROBE_DIR else ""
-    obj = os.path.join(OBJDIR, sub + os.path.basename(src)[:-4] + ".o")
+    obj = os.path.join(objdir, sub + os.path.basename(src)[:-4] + ".o")
     cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
@@ -79,5 +79,26 @@ def build(verbose=False, jobs=None):
     return LIBRARY
 
 
+def build_tree(csrc, library):
+    """Build the path's library from another source tree (for instance an
+    earlier commit's ``akas_amd/csrc``, from ``git archive``) into
+    ``library``, with this build's flags; for timing builds side by side."""
+    objdir = os.path.join(os.path.dirname(os.path.abspath(library)), "_obj")
+    os.makedirs(objdir, exist_ok=True)
+    srcs = sources(csrc)
+    with ThreadPoolExecutor(max_workers=min(len(srcs), os.cpu_count() or 2)) as pool:
+        objs = list(pool.map(lambda s: _compile(s, objdir), srcs))
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-Bsymbolic-functions", *objs,
+           "-o", library]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
+    shutil.rmtree(objdir)
+    return library
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    if len(sys.argv) == 4 and sys.argv[1] == "--tree":
+        print(build_tree(sys.argv[2], sys.argv[3]))
+    else:
+        build(verbose=True)

@@ -455,7 +455,7 @@ __global__ __launch_bounds__(64 * kSplitQuarters * MH) void dense_split_kernel(D
 // wave's 128 output columns are either all inside the matrix or all outside;
 // rows and columns past the ends are clamped on load and never stored.
 // ---------------------------------------------------------------------------
-template <int OUT>
+template <int OUT, int SDT>
 __global__ __launch_bounds__(dma::THREADS) void dense_dma_kernel(DenseArgs p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -488,24 +488,35 @@ __global__ __launch_bounds__(dma::THREADS) void dense_dma_kernel(DenseArgs p) {
   const int a_row0 = (wave & 3) * 64, b_row0 = (wave >> 2) * 128;
   const int col0 = n0 + b_row0;
   const bool live = m0 + a_row0 < p.M && col0 < p.N;  // wave-uniform
-  // The weight scales of the tile's two 128-column blocks over this
-  // partition's k-blocks, as float32 (either scale dtype gives the same main
-  // loop).
-  const int nkb = kb1 - kb0;
-  for (int i = tid; i < 2 * nkb; i += dma::THREADS) {
-    const int h = i / nkb, k = kb0 + i % nkb;
-    const int64_t at = (int64_t)min((n0 + 128 * h) / kBlock, (p.N - 1) / kBlock) * KB + k;
-    dma::wtab[h][i % nkb] = p.ws_dtype == AKAS_DTYPE_F32 ? load_scale_t<AKAS_DTYPE_F32>(p.ws, at)
-                                                         : load_scale_t<AKAS_DTYPE_BF16>(p.ws, at);
-  }
-  __syncthreads();
-  const float* wrow = dma::wtab[wave >> 2];
+  // Weight scale of each k-block for this wave's 128-column block.  f32
+  // scales are loaded per stage from global memory, so the first stage's
+  // copies go out at once (a table in LDS first costs a load round trip per
+  // tile: 2,011-2,046 against 2,041-2,068 TFLOP/s at M=8192, K=2048,
+  // N=6144).  bf16 scales go through a float32 table in LDS over the
+  // partition's k-blocks, because a bf16 load per stage made the compiler
+  // spill in the main loop.
   dma::Acc acc;
   acc.clear();
-  dma::run<false>(plan, acc, a_row0, b_row0, kb0, kb1, lane, [&](int kb) {
-    const float w = wrow[kb - kb0];
-    return float2{w, w};
-  }, live);
+  if constexpr (SDT == AKAS_DTYPE_F32) {
+    const int64_t ws_base = (int64_t)min(col0 / kBlock, (p.N - 1) / kBlock) * KB;
+    dma::run<false>(plan, acc, a_row0, b_row0, kb0, kb1, lane, [&](int kb) {
+      const float w = load_scale_t<AKAS_DTYPE_F32>(p.ws, ws_base + kb);
+      return float2{w, w};
+    }, live);
+  } else {
+    const int nkb = kb1 - kb0;
+    for (int i = tid; i < 2 * nkb; i += dma::THREADS) {
+      const int h = i / nkb, k = kb0 + i % nkb;
+      const int64_t at = (int64_t)min((n0 + 128 * h) / kBlock, (p.N - 1) / kBlock) * KB + k;
+      dma::wtab[h][i % nkb] = load_scale_t<AKAS_DTYPE_BF16>(p.ws, at);
+    }
+    __syncthreads();
+    const float* wrow = dma::wtab[wave >> 2];
+    dma::run<false>(plan, acc, a_row0, b_row0, kb0, kb1, lane, [&](int kb) {
+      const float w = wrow[kb - kb0];
+      return float2{w, w};
+    }, live);
+  }
   const int64_t obase = (int64_t)part * p.part_stride + col0;
   dma::store_tile<OUT>(
       acc, p.out, wave, lane, [&](int r) { return m0 + a_row0 + r < p.M && col0 < p.N; },
@@ -903,7 +914,7 @@ static void launch_split_m(const DenseArgs& a, int parts, hipStream_t s) {
 template <int OUT, int SDT>
 static void launch_dma(const DenseArgs& a, int parts, hipStream_t s) {
   const int tiles = ((a.M + dma::BM - 1) / dma::BM) * ((a.N + dma::BN - 1) / dma::BN);
-  dense_dma_kernel<OUT><<<dim3(tiles, parts), dma::THREADS, 0, s>>>(a);
+  dense_dma_kernel<OUT, SDT><<<dim3(tiles, parts), dma::THREADS, 0, s>>>(a);
 }
 
 // The direct-load small-M kernel (up to 64 rows) by its row count.

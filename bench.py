@@ -29,6 +29,7 @@ config).
                                   # launches for rocprofv3 --pmc passes
     python bench.py --roofline-probe   # the measured ceilings alone
     python bench.py --operand-probe    # prefill GEMM: random against constant operands
+    python bench.py --library-ab LIB [LIB ...]   # prefill GEMMs, library builds interleaved
 """
 
 import argparse
@@ -558,6 +559,47 @@ def kernel_probe(torch, dev, what):
     print(json.dumps(info))
 
 
+def library_ab(torch, dev, paths, rounds=6, launches=10):
+    """The three prefill GEMM launches (M=8192, bf16 out, on prequantized
+    codes) with each library in ``paths`` in turn, ``rounds`` times, all in
+    one process on one GPU: builds compared on the same box and inputs.  A
+    library is bound by its own entry points (``projection_partial``,
+    ``quantize``), which every build of this path exports with the same
+    signatures.  Prints one line per round and library, TFLOP/s per shape."""
+    import ctypes
+
+    from akas_amd import _lib, ops
+
+    libs = []
+    for path in paths:
+        lib = ctypes.CDLL(path)
+        for name in ("akas_quantize", "akas_projection_partial", "akas_quantize_weight_blocks",
+                     "akas_status_string"):
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = _lib.SIGNATURES[name]
+        libs.append(lib)
+    bound = _lib._LIB
+    inputs = []
+    for (k, n) in PREFILL_SHAPES:
+        codes, scales = make_weights(torch, n, k, 1, 7 + n, dev)
+        x = bf16_activations(torch, 8192, k, 99, dev, outliers=0.0)
+        q, qs = ops.quantize(x)
+        inputs.append((k, n, codes[0], scales[0], q, qs,
+                       torch.empty((8192, n), dtype=torch.bfloat16, device=dev)))
+    try:
+        for r in range(rounds):
+            for path, lib in zip(paths, libs):
+                _lib._LIB = lib
+                row = dict(round=r, library=path)
+                for (k, n, w, s, q, qs, out) in inputs:
+                    ms = time_kernel_graph(torch, lambda i: ops.projection_partial(
+                        q, qs, w, s, out=out, out_dtype=torch.bfloat16), launches)
+                    row[f"K{k}_N{n}"] = round(2 * 8192 * k * n / (ms * 1e-3) / 1e12, 1)
+                print(json.dumps(row), flush=True)
+    finally:
+        _lib._LIB = bound
+
+
 OPERAND_CODES = {"random": None, "zero": 0x00, "one": 0x38, "max": 0x7E}
 
 
@@ -677,6 +719,8 @@ def main():
                     help="only measure the streaming-read and FP8 MFMA ceilings")
     ap.add_argument("--operand-probe", action="store_true",
                     help="only time the prefill GEMM on random against constant operands")
+    ap.add_argument("--library-ab", nargs="+", metavar="LIB", default=None,
+                    help="only time the prefill GEMMs with each of these library builds in turn")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported "
@@ -700,6 +744,9 @@ def main():
         return
     if args.operand_probe:
         operand_probe(torch, dev)
+        return
+    if args.library_ab:
+        library_ab(torch, dev, args.library_ab)
         return
 
     dec = decode_sweep(torch, dev, args.steps, args.warmup)
