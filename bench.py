@@ -30,6 +30,7 @@ config).
     python bench.py --roofline-probe   # the measured ceilings alone
     python bench.py --operand-probe    # prefill GEMM: random against constant operands
     python bench.py --library-ab LIB [LIB ...]   # prefill GEMMs, library builds interleaved
+    python bench.py --vendor-probe     # prefill GEMM beside hipBLASLt's FP8 GEMMs
 """
 
 import argparse
@@ -600,6 +601,49 @@ def library_ab(torch, dev, paths, rounds=6, launches=10):
         _lib._LIB = bound
 
 
+def vendor_probe(torch, dev, rounds=4, reps=20):
+    """hipBLASLt's FP8 GEMMs (``torch._scaled_mm`` with one scale per tensor,
+    or one per row and column, applied once after the k-loop) beside this
+    library's block-scaled GEMM launch, on the three prefill shapes and the
+    same e4m3 codes, rounds interleaved in one process.  The vendor kernels
+    skip the per-k-block scale fold that 1x128 / 128x128 block scales need,
+    so they bound what an FP8 GEMM of these shapes reaches on this chip and
+    data.  Prints one line per round, TFLOP/s per shape and kernel."""
+    from akas_amd import ops
+
+    inputs = []
+    for (k, n) in PREFILL_SHAPES:
+        codes, scales = make_weights(torch, n, k, 1, 7 + n, dev)
+        x = bf16_activations(torch, 8192, k, 99, dev, outliers=0.0)
+        q, qs = ops.quantize(x)
+        inputs.append((k, n, codes[0], scales[0], q, qs,
+                       torch.empty((8192, n), dtype=torch.bfloat16, device=dev)))
+    one = torch.ones((), dtype=torch.float32, device=dev)
+    for r in range(rounds):
+        row = dict(round=r)
+        for (k, n, w, s, q, qs, out) in inputs:
+            flops = 2 * 8192 * k * n
+            a8 = q.view(torch.float8_e4m3fn)
+            b8 = w.view(torch.float8_e4m3fn).t()  # column-major [K, N]
+            kernels = {
+                "akas_gemm": lambda i: ops.projection_partial(q, qs, w, s, out=out, out_dtype=torch.bfloat16),
+                "hipblaslt_tensorwise": lambda i: torch._scaled_mm(a8, b8, scale_a=one, scale_b=one,
+                                                                   out_dtype=torch.bfloat16),
+                "hipblaslt_rowwise": lambda i: torch._scaled_mm(
+                    a8, b8, scale_a=torch.ones((8192, 1), dtype=torch.float32, device=dev),
+                    scale_b=torch.ones((1, n), dtype=torch.float32, device=dev), out_dtype=torch.bfloat16),
+            }
+            for name, fn in kernels.items():
+                try:
+                    fn(0)
+                    torch.cuda.synchronize()
+                    ms = time_kernel(torch, fn, reps)
+                    row[f"K{k}_N{n}_{name}"] = round(flops / (ms * 1e-3) / 1e12, 1)
+                except RuntimeError as e:  # a refusal by the library, not a GPU fault
+                    row[f"K{k}_N{n}_{name}"] = f"unavailable: {str(e)[:120]}"
+        print(json.dumps(row), flush=True)
+
+
 OPERAND_CODES = {"random": None, "zero": 0x00, "one": 0x38, "max": 0x7E}
 
 
@@ -719,6 +763,8 @@ def main():
                     help="only measure the streaming-read and FP8 MFMA ceilings")
     ap.add_argument("--operand-probe", action="store_true",
                     help="only time the prefill GEMM on random against constant operands")
+    ap.add_argument("--vendor-probe", action="store_true",
+                    help="only time hipBLASLt's FP8 GEMMs beside the prefill GEMM launch")
     ap.add_argument("--library-ab", nargs="+", metavar="LIB", default=None,
                     help="only time the prefill GEMMs with each of these library builds in turn")
     args = ap.parse_args()
@@ -747,6 +793,9 @@ def main():
         return
     if args.library_ab:
         library_ab(torch, dev, args.library_ab)
+        return
+    if args.vendor_probe:
+        vendor_probe(torch, dev)
         return
 
     dec = decode_sweep(torch, dev, args.steps, args.warmup)
