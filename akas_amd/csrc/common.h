@@ -136,10 +136,13 @@ AKAS_DEV uint32_t f32_to_bf16_bits(float v) {
   return (uint32_t)__builtin_bit_cast(uint16_t, h);
 }
 
-// Two values packed low/high with one v_cvt_pk_bf16_f32.
+// Two values packed low/high with one v_cvt_pk_bf16_f32 (round to nearest
+// even, as the scalar conversion; converting the halves one at a time costs
+// two conversions, a shift and an or).
 AKAS_DEV uint32_t f32x2_to_bf16x2(float lo, float hi) {
-  const __bf16 a = (__bf16)lo, b = (__bf16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
 AKAS_DEV float round_bf16(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
@@ -164,6 +167,15 @@ AKAS_DEV uint32_t f32_to_f16_bits(float v) {
 }
 
 AKAS_DEV float round_f16(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
+
+// Two values packed low/high with one v_cvt_pk_f16_f32 (round to nearest
+// even), each first fixed in a register as f32_to_f16_bits does.
+AKAS_DEV uint32_t f32x2_to_f16x2(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  asm volatile("" : "+v"(lo), "+v"(hi));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, f16x2));
+}
 
 AKAS_DEV float round_to(float v, int dtype) {
   return dtype == AKAS_DTYPE_BF16 ? round_bf16(v) : (dtype == AKAS_DTYPE_F16 ? round_f16(v) : v);

@@ -517,10 +517,9 @@ __global__ __launch_bounds__(dma::THREADS) void dense_dma_kernel(DenseArgs p) {
       return float2{w, w};
     }, live);
   }
-  const int64_t obase = (int64_t)part * p.part_stride + col0;
-  dma::store_tile<OUT>(
-      acc, p.out, wave, lane, [&](int r) { return m0 + a_row0 + r < p.M && col0 < p.N; },
-      [&](int r) { return obase + (int64_t)(m0 + a_row0 + r) * p.ldo; });
+  const int rows = col0 < p.N ? min(64, p.M - (m0 + a_row0)) : 0;
+  dma::store_tile_rows<OUT>(acc, p.out, wave, lane, rows,
+                            (int64_t)part * p.part_stride + col0 + (int64_t)(m0 + a_row0) * p.ldo, p.ldo);
 }
 
 // ---------------------------------------------------------------------------

@@ -167,8 +167,8 @@ AKAS_DEV void store_out4(void* out, int64_t i, const v4f& v) {
       q.x = f32x2_to_bf16x2(v[0], v[1]);
       q.y = f32x2_to_bf16x2(v[2], v[3]);
     } else {
-      q.x = f32_to_f16_bits(v[0]) | (f32_to_f16_bits(v[1]) << 16);
-      q.y = f32_to_f16_bits(v[2]) | (f32_to_f16_bits(v[3]) << 16);
+      q.x = f32x2_to_f16x2(v[0], v[1]);
+      q.y = f32x2_to_f16x2(v[2], v[3]);
     }
     *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(out) + i) = q;
   }

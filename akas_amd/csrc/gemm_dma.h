@@ -232,7 +232,7 @@ AKAS_DEV void run(const Plan& p, Acc& acc, int a_row0, int b_row0, int kb0, int 
 }
 
 AKAS_DEV uint32_t pack2(float lo, float hi, int dt) {
-  return dt == AKAS_DTYPE_BF16 ? f32x2_to_bf16x2(lo, hi) : (f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16));
+  return dt == AKAS_DTYPE_BF16 ? f32x2_to_bf16x2(lo, hi) : f32x2_to_f16x2(lo, hi);
 }
 
 // Write the wave's 64x128 tile.  16-bit outputs go through a per-wave 16 KB
@@ -276,6 +276,53 @@ AKAS_DEV void store_tile(const Acc& acc, void* out, int wave, int lane, RowOk ro
       const int r = it * 4 + (lane >> 4), ch = lane & 15;
       const u32x4 v = *reinterpret_cast<const u32x4*>(region + r * 256 + ((ch ^ (r & 15)) << 4));
       if (row_ok(r)) *reinterpret_cast<u32x4*>(o + out_row(r) + ch * 8) = v;
+    }
+  }
+}
+
+// store_tile for a wave whose row r (0..63) goes to element offset
+// first + r * ldo and exists when r < rows: each lane's address is formed
+// once and advanced by a constant stride, instead of once per store.  The
+// 16-bit path stages through the wave's own LDS region (as store_tile), so
+// only the wave's own order matters there: its LDS accesses complete in
+// issue order, and the fence keeps the compiler from moving the reads above
+// the writes.  Must follow the main loop's closing barrier.
+template <int OUT>
+AKAS_DEV void store_tile_rows(const Acc& acc, void* out, int wave, int lane, int rows, int64_t first, int64_t ldo) {
+  if constexpr (OUT == AKAS_DTYPE_F32) {
+    float* o = reinterpret_cast<float*>(out) + first + (int64_t)(lane & 15) * ldo + 4 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (16 * i + (lane & 15) < rows) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          *reinterpret_cast<float4*>(o + 16 * j) =
+              float4{acc.t[i][j][0], acc.t[i][j][1], acc.t[i][j][2], acc.t[i][j][3]};
+      }
+      o += 16 * ldo;
+    }
+  } else {
+    uint8_t* region = (wave < 4 ? stage0 : stage1) + (wave & 3) * 16384;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int r = 16 * i + (lane & 15);
+        const int col = 16 * j + 4 * (lane >> 4);
+        uint2 v;
+        v.x = pack2(acc.t[i][j][0], acc.t[i][j][1], OUT);
+        v.y = pack2(acc.t[i][j][2], acc.t[i][j][3], OUT);
+        *reinterpret_cast<uint2*>(region + r * 256 + (((col >> 3) ^ (r & 15)) << 4) + (col & 7) * 2) = v;
+      }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const int ch = lane & 15;
+    uint16_t* o = reinterpret_cast<uint16_t*>(out) + first + (int64_t)(lane >> 4) * ldo + ch * 8;
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      const int r = it * 4 + (lane >> 4);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(region + r * 256 + ((ch ^ (r & 15)) << 4));
+      if (r < rows) *reinterpret_cast<u32x4*>(o) = v;
+      o += 4 * ldo;
     }
   }
 }

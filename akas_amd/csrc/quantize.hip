@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void rms_quantize_kernel(const void* __restric
 #pragma unroll
           for (int i = 0; i < 4; ++i)
             u[i] = YT == AKAS_DTYPE_BF16 ? f32x2_to_bf16x2(qv[2 * i], qv[2 * i + 1])
-                                         : (f32_to_f16_bits(qv[2 * i]) | (f32_to_f16_bits(qv[2 * i + 1]) << 16));
+                                         : f32x2_to_f16x2(qv[2 * i], qv[2 * i + 1]);
           *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(y) + rbase + col) = pk;
         }
       }
