@@ -477,6 +477,58 @@ def test_fp8_linear_prequantized_binding(dev, m):
         ops.fp8_linear(_t(x, dev, torch.bfloat16), w, s, xs)
 
 
+def test_fp8_linear_graph_replays(dev):
+    """fp8_linear at every kernel path (fused wide, split with its quantizer,
+    deep-k partitions and merge, tiled, the DMA-fed prefill tiles, and the
+    entry point without allocation) captured in one HIP graph, as a decode
+    or prefill program captures a step: every replay, each on new input
+    values written between replays and with eager calls and
+    synchronizations in between, equals the eager result bit for bit."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(57)
+    shapes = [(1, 2048, 6144), (16, 2048, 6144), (256, 2048, 6144), (64, 4096, 2048),
+              (300, 512, 1024), (4096, 2048, 4096)]
+    cases = []
+    for m, k, n in shapes:
+        codes, scales = block_weights(rng, (n, k))
+        x = _t(bf16_normal(rng, (m, k), outliers=0.01), dev, torch.bfloat16)
+        cases.append((x, _t(codes, dev), _t(scales, dev),
+                      torch.empty((m, n), dtype=torch.bfloat16, device=dev)))
+    m0, k0, n0 = shapes[0]
+    noalloc_out = torch.empty((m0, n0), dtype=torch.bfloat16, device=dev)
+
+    def step():
+        for x, w, s, out in cases:
+            ops.fp8_linear(x, w, s, out=out)
+        x, w, s, _ = cases[0]
+        ops.fp8_linear_noalloc(x, w, s, out=noalloc_out)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm the per-stream caches outside capture
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for rep in range(3):
+        for x, _, _, out in cases:
+            x.copy_(_t(bf16_normal(rng, tuple(x.shape), outliers=0.01), dev, torch.bfloat16))
+            out.zero_()
+        noalloc_out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        got = [out.clone() for *_, out in cases] + [noalloc_out.clone()]
+        step()  # eager on the same inputs, between replays
+        torch.cuda.synchronize()
+        for (_, _, _, out), r in zip(cases, got):
+            assert torch.equal(r, out), rep
+        assert torch.equal(got[-1], cases[0][3]), rep
+
+
 def test_linear_workspace_cache_is_bounded(dev):
     """Calls cycling through more streams than the per-device cache keeps
     leave at most that many workspaces cached, and every result equals the
