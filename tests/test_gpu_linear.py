@@ -529,6 +529,32 @@ def test_fp8_linear_graph_replays(dev):
         assert torch.equal(got[-1], cases[0][3]), rep
 
 
+def test_zero_row_calls(dev):
+    """Empty batches (zero rows) through the dense entry points: each returns
+    correctly shaped empty outputs without error, and a later non-empty call
+    on the same stream is unaffected."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(61)
+    codes, scales = block_weights(rng, (512, 1024))
+    w, s = _t(codes, dev), _t(scales, dev)
+    x0 = torch.empty((0, 1024), dtype=torch.bfloat16, device=dev)
+    q, qs = ops.quantize(x0)
+    assert tuple(q.shape) == (0, 1024) and tuple(qs.shape) == (0, 8)
+    assert tuple(ops.fp8_linear(x0, w, s, out_dtype=torch.bfloat16).shape) == (0, 512)
+    assert tuple(ops.fp8_linear(q, w, s, qs).shape) == (0, 512)
+    assert tuple(ops.projection_partial(q, qs, w, s).shape) == (0, 512)
+    assert tuple(ops.fp8_linear_noalloc(x0, w, s, out_dtype=torch.bfloat16).shape) == (0, 512)
+    norm_w = _t(np.ones(1024, np.float32), dev)
+    rc, rs, rn = ops.rms_quantize(x0, norm_w, eps=1e-6)
+    assert tuple(rc.shape) == (0, 1024) and tuple(rs.shape) == (0, 8) and tuple(rn.shape) == (0, 1024)
+    x = bf16_normal(rng, (5, 1024))
+    y = ops.fp8_linear(_t(x, dev, torch.bfloat16), w, s, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert rel_fro(y.cpu().numpy(), ofp8.fp8_linear(x, codes, scales)) < 1e-4
+
+
 def test_linear_workspace_cache_is_bounded(dev):
     """Calls cycling through more streams than the per-device cache keeps
     leave at most that many workspaces cached, and every result equals the
