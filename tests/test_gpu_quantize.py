@@ -117,6 +117,42 @@ def test_quantize_midpoints_and_subnormals(dev):
     np.testing.assert_array_equal(c, ec)
 
 
+def test_quantize_group_scale_every_mantissa(dev):
+    """The group scale max(max|x|, 1e-12) / 448 is the oracle's float32
+    division for every float32 mantissa, at the exponent where the 1e-12
+    floor sits, at two ordinary exponents and at the largest finite one, and
+    at the ends of the range: groups holding one value (either sign) among
+    zeros, through quantize.  (The device forms it without a division
+    sequence, from RN(1/448) and one FMA correction.)"""
+    import torch
+    from akas_amd import ops
+
+    n = 1 << 21
+    mant = torch.arange(1 << 23, dtype=torch.int32, device=dev)
+    for e in (87, 107, 130, 254):  # biased exponents: 2^-40, 2^-20, 2^3, 2^127
+        for c0 in range(0, 1 << 23, n):
+            a = (mant[c0:c0 + n] | (e << 23)).view(torch.float32)
+            x = torch.zeros((n, 128), dtype=torch.float32, device=dev)
+            x[:, 37] = a
+            x[::2, 37] *= -1
+            _, s = ops.quantize(x)
+            got = s.view(-1).cpu().numpy()
+            want = ofp8.group_scales(x[:, 37:38].cpu().numpy())
+            bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+            assert bad.size == 0, (e, c0 + bad[:8], got[bad[:8]], want[bad[:8]])
+    f32 = np.finfo(np.float32)
+    ends = np.array([0.0, 1e-45, 1e-13, np.nextafter(np.float32(1e-12), 0), 1e-12,
+                     np.nextafter(np.float32(1e-12), 1), 1.0, 448.0, f32.max, np.inf], np.float32)
+    x = np.zeros((ends.size, 128), np.float32)
+    x[:, 5] = ends
+    c, s, ec, es = _run(x, "float32", dev)
+    np.testing.assert_array_equal(s.view(np.uint32), es.view(np.uint32))
+    # inf / inf is a NaN whose sign is the platform's: magnitude code only
+    finite = np.isfinite(x)
+    np.testing.assert_array_equal(c[finite], ec[finite])
+    assert (c[~finite] & 0x7F == 126).all() and (ec[~finite] & 0x7F == 126).all()
+
+
 def test_dequantize_round_trip(dev):
     import torch
     from akas_amd import ops
