@@ -80,11 +80,15 @@ AKAS_DEV void unpack8(const Raw8& r, float v[8]) {
 //
 // The 16-lane maximum is four DPP row operations (quad swaps, then the
 // half-row and row mirrors), which stay in the VALU instead of going
-// through the LDS crossbar as lane shuffles do.
+// through the LDS crossbar as lane shuffles do.  The lane maxima are
+// non-negative and never a quiet NaN (the lane's own maximum skips one), so
+// the unsigned maximum of their bit patterns is their float maximum; it
+// folds each DPP move into a v_max_u32_dpp.
 template <int CTRL>
 AKAS_DEV float dpp_max(float m) {
-  const float o = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), CTRL, 0xF, 0xF, true));
-  return __builtin_fmaxf(m, o);
+  const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, __float_as_int(m), CTRL, 0xF, 0xF, true);
+  const uint32_t b = __float_as_uint(m);
+  return __uint_as_float(b > o ? b : o);
 }
 
 AKAS_DEV float row16_max(float m) {
