@@ -16,8 +16,9 @@ Also reported: ``roofline`` for the dominant op of the step (the M=256
 ``fp8_linear``, every launch it makes), ``roofline_prefill`` for the
 prefill ``fp8_linear`` op at M=8192, K=2048, N=6144 (its quantizer and GEMM
 launches; MFMA-bound), ``ceilings`` measured by the probe library
-(streaming HBM read, FP8 MFMA), ``extras`` (the prefill GEMMs, the MoE
-decode layer unpacked and packed, the skewed MoE prefill layer, the fused RMSNorm + quantizer
+(streaming HBM read, FP8 MFMA), ``extras`` (the single M=16, K=N=2048 linear
+the reference's CPU path runs, the prefill GEMMs, the MoE decode layer
+unpacked and packed, the skewed MoE prefill layer, the fused RMSNorm + quantizer
 and the shared-expert MoE block; each MoE block timed as one of four
 captured back to back in a graph, as a decode step graph holds many layers)
 and ``cpu_baseline`` (the oracle's C restatement on the host cores, per
@@ -340,6 +341,28 @@ def shared_expert_block_bench(torch, dev, tokens=64, steps=10):
                 gbs=round(wbytes / (ms * 1e-3) / 1e9, 1),
                 frac_hbm=round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                 active_experts=active_experts)
+
+
+def config1_linear_bench(torch, dev, m=16, k=2048, n=2048):
+    """The single linear the reference's CPU path runs (M=16, K=N=2048, bf16
+    in and out, f32 block scales): one ``fp8_linear`` op per launch, each on
+    its own weight copy from a rotation of more than twice the last-level
+    cache, so the weights stream from HBM as in the decode sweep."""
+    from akas_amd import ops
+
+    copies = math.ceil(2 * LLC_BYTES / (n * k)) + 1
+    codes, scales = make_weights(torch, n, k, copies, 4321, dev)
+    x = bf16_activations(torch, m, k, 7, dev)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    ws = ops.linear_workspace(m, k, n, dev)
+    us = time_kernel_graph(torch, lambda i: ops.fp8_linear(
+        x, codes[i % copies], scales[i % copies], out=out, workspace=ws), copies) * 1e3
+    nbytes = dense_bytes(m, k, n)
+    del codes, scales
+    return dict(M=m, K=k, N=n, us=round(us, 3), bytes=nbytes,
+                gbs=round(nbytes / (us * 1e-6) / 1e9, 1),
+                frac_hbm=round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                tflops=round(2 * m * n * k / (us * 1e-6) / 1e12, 2))
 
 
 def rms_quantize_bench(torch, dev, rows=16384, cols=2048, steps=20):
@@ -838,6 +861,7 @@ def main():
             mfma_busy_frac=busy,
             counters_source=f"profiles/{PREFILL_COUNTERS}" if busy or traffic else None)
         line["extras"] = dict(
+            config1_linear=config1_linear_bench(torch, dev),
             prefill_gemm=prefill,
             moe_decode=moe_layer_bench(torch, dev, 256, False, 20),
             moe_decode_packed=moe_layer_bench(torch, dev, 256, False, 20, packed=True),
