@@ -16,8 +16,9 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "akas_amd", "csrc")
 LIBDIR = os.path.join(ROOT, "akas_amd", "lib")
 LIBRARY = os.path.join(LIBDIR, "libakas_fp8.so")
-# Roofline probes (HBM streaming read, FP8 MFMA peak) for the benchmark, in a
-# library of their own: they are measurement tools, not part of the path.
+# Probes in a library of their own, not part of the path: the roofline
+# ceilings the benchmark reports (HBM streaming read, FP8 MFMA peak, the split
+# GEMM's loads) and an exhaustive numerics check the tests run.
 PROBE_DIR = os.path.join(CSRC, "probe")
 PROBE_LIBRARY = os.path.join(LIBDIR, "libakas_probe.so")
 OBJDIR = os.path.join(ROOT, "_build")

@@ -78,10 +78,10 @@ struct GroupScale {
 //   s = RN(a / 448) by the same correction, with RN(1/448) as a constant;
 //   r = RN(1 / s) by one Newton step from v_rcp_f32, e = 1 - s*y0 (exact
 //   through fma), r = RN(y0 + e*y0).
-// Each equals IEEE float32 division for every input it can receive (s for
-// every float32 a in [1e-12, FLT_MAX], r for every normal s up to 2^126;
-// scales lie in [2^-49, 2^120]), compared exhaustively on gfx950.  An
-// infinite maximum gives s = inf and r = c = 0, as the divisions do.
+// Each equals IEEE float32 division for every input it can receive (every
+// float32 a in [1e-12, FLT_MAX], whose scales cover [2^-49, 2^120]),
+// compared exhaustively on gfx950 by the numerics probe (probe/numerics.hip).
+// An infinite maximum gives s = inf and r = c = 0, as the divisions do.
 AKAS_DEV GroupScale make_group_scale(float amax) {
 #pragma clang fp contract(off)
   constexpr float kInv448 = 0x1.24924ap-9f;  // RN(1/448)

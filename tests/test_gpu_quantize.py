@@ -153,6 +153,25 @@ def test_quantize_group_scale_every_mantissa(dev):
     assert (c[~finite] & 0x7F == 126).all() and (ec[~finite] & 0x7F == 126).all()
 
 
+def test_group_scale_every_input(dev):
+    """The device's group scale and its reciprocal (formed without a division
+    sequence) equal IEEE float32 division for every group maximum from the
+    1e-12 floor to FLT_MAX and for +inf: the numerics probe runs the same
+    device function over all of them (about 360 million inputs)."""
+    import ctypes
+
+    import torch
+    from akas_amd import build
+
+    lib = ctypes.CDLL(build.PROBE_LIBRARY)
+    lib.akas_probe_group_scale_check.restype = ctypes.c_int
+    lib.akas_probe_group_scale_check.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    out = torch.zeros(9, dtype=torch.int64, device=dev)
+    assert lib.akas_probe_group_scale_check(out.data_ptr(), torch.cuda.current_stream().cuda_stream) == 0
+    res = out.cpu().numpy()
+    assert res[0] == 0, [hex(int(b)) for b in res[1:1 + min(int(res[0]), 8)]]
+
+
 def test_dequantize_round_trip(dev):
     import torch
     from akas_amd import ops
