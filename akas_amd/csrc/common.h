@@ -121,9 +121,9 @@ AKAS_DEV float scaled_quotient(float x, const GroupScale& g) {
 // Hardware OCP-e4m3 conversion of two values into the low (HI=false) or high
 // (HI=true) 16 bits of `old`.  For |v| < 464 it is bit-identical to the
 // reference encoder (src/akas/quantization/_shared/e4m3.py:16-29), ties,
-// subnormals and signed zero included -- established by an exhaustive
-// comparison over every float32 pattern in that range on gfx950; above 464
-// it would produce NaN, which scaled_quotient() rules out.
+// subnormals and signed zero included -- compared over every float32
+// pattern in that range on gfx950 by the numerics probe (probe/numerics.hip);
+// above 464 it would produce NaN, which scaled_quotient() rules out.
 template <bool HI>
 AKAS_DEV uint32_t cvt_e4m3x2(float a, float b, uint32_t old) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, (int)old, HI);
@@ -145,7 +145,8 @@ AKAS_DEV float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16
 // Round to nearest even (src/akas/quantization/_shared/rounding.py:43-54,
 // the integer form (bits + 0x7FFF + lsb) >> 16).  gfx950's v_cvt_pk_bf16_f32
 // gives the same bits as that integer form for every non-NaN f32 pattern,
-// denormals included (compared over all 2^32 patterns on the GPU), and
+// denormals included (compared over all 2^32 patterns on the GPU by the
+// numerics probe, probe/numerics.hip), and
 // costs one instruction per two values.
 AKAS_DEV uint32_t f32_to_bf16_bits(float v) {
   const __bf16 h = (__bf16)v;

@@ -153,23 +153,45 @@ def test_quantize_group_scale_every_mantissa(dev):
     assert (c[~finite] & 0x7F == 126).all() and (ec[~finite] & 0x7F == 126).all()
 
 
-def test_group_scale_every_input(dev):
-    """The device's group scale and its reciprocal (formed without a division
-    sequence) equal IEEE float32 division for every group maximum from the
-    1e-12 floor to FLT_MAX and for +inf: the numerics probe runs the same
-    device function over all of them (about 360 million inputs)."""
+def _numerics_probe(dev, name):
+    """Run an exhaustive check of the numerics probe (libakas_probe.so):
+    returns the mismatch count and the first mismatching bit patterns."""
     import ctypes
 
     import torch
     from akas_amd import build
 
-    lib = ctypes.CDLL(build.PROBE_LIBRARY)
-    lib.akas_probe_group_scale_check.restype = ctypes.c_int
-    lib.akas_probe_group_scale_check.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    fn = getattr(ctypes.CDLL(build.PROBE_LIBRARY), name)
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     out = torch.zeros(9, dtype=torch.int64, device=dev)
-    assert lib.akas_probe_group_scale_check(out.data_ptr(), torch.cuda.current_stream().cuda_stream) == 0
+    assert fn(out.data_ptr(), torch.cuda.current_stream().cuda_stream) == 0
     res = out.cpu().numpy()
-    assert res[0] == 0, [hex(int(b)) for b in res[1:1 + min(int(res[0]), 8)]]
+    return int(res[0]), [hex(int(b)) for b in res[1:1 + min(int(res[0]), 8)]]
+
+
+def test_group_scale_every_input(dev):
+    """The device's group scale and its reciprocal (formed without a division
+    sequence) equal IEEE float32 division for every group maximum from the
+    1e-12 floor to FLT_MAX and for +inf: the numerics probe runs the same
+    device function over all of them (about 360 million inputs)."""
+    n, first = _numerics_probe(dev, "akas_probe_group_scale_check")
+    assert n == 0, first
+
+
+def test_e4m3_hardware_pack_every_input(dev):
+    """The hardware e4m3 pack the quantizers use equals the integer
+    restatement of the reference encoder (_shared/e4m3.py:16-29) for every
+    float32 of magnitude below 464, both signs (about 2.3 billion inputs)."""
+    n, first = _numerics_probe(dev, "akas_probe_e4m3_pack_check")
+    assert n == 0, first
+
+
+def test_bf16_hardware_pack_every_input(dev):
+    """The packed bf16 conversion equals the reference's integer round to
+    nearest even (_shared/rounding.py:43-54) for every non-NaN float32."""
+    n, first = _numerics_probe(dev, "akas_probe_bf16_pack_check")
+    assert n == 0, first
 
 
 def test_dequantize_round_trip(dev):
