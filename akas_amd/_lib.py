@@ -57,6 +57,9 @@ SIGNATURES = {
     "akas_swiglu_experts": (_i, [_p, _p, _i, _p, _i, _i64, _i, _i64, _i, _i, _i, _p]),
     "akas_moe_combine": (_i, [_p, _i, _p, _p, _i, _p, _i, _p, _i64, _i, _i64, _p]),
     "akas_routed_combine": (_i, [_p, _i, _p, _p, _p, _i64, _i, _i64, _p]),
+    "akas_shared_expert_moe_workspace_size": (_sz, [_i64, _i, _i, _i64, _i64]),
+    "akas_shared_expert_moe": (_i, [_p, _i, _p, _p, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                                    _p, _p, _i, _p, _p, _sz, _i64, _i, _i, _i64, _i64, _p]),
 }
 
 _LIB = None

@@ -22,6 +22,7 @@
 #include "device_info.h"
 #include "gemm_core.h"
 #include "gemm_dma.h"
+#include "moe_launch.h"
 #include "quant_group.h"
 
 namespace akas {
@@ -33,6 +34,13 @@ struct ExpertArgs {
   const void* ws;      // [E, NB, KB] block scales
   const uint8_t* w2;   // up codes (paired)
   const void* ws2;     // up block scales (paired)
+  // An expert outside the bank: when xw is set, expert E-1 takes its codes
+  // and scales from these ([N, K], [NB, KB]; xw2/xws2 the up half when
+  // paired) and the bank holds experts 0 .. E-2.
+  const uint8_t* xw;
+  const void* xws;
+  const uint8_t* xw2;
+  const void* xws2;
   const int32_t* counts;
   const int32_t* routes;   // [E, r]
   const int32_t* offsets;  // expert_offsets (packed input/output)
@@ -98,6 +106,28 @@ AKAS_DEV void locate_tile(const int32_t* counts, int experts, int bm, int t, int
     }
     base += __shfl(incl, 63, 64);
   }
+}
+
+// Codes and block scales of expert e: the bank's slice, or the expert kept
+// outside the bank (its scale index then starts at expert 0).
+struct ExpertSlice {
+  const uint8_t* w;
+  const uint8_t* w2;
+  const void* ws;
+  const void* ws2;
+  int scale_expert;
+};
+
+AKAS_DEV ExpertSlice expert_slice(const ExpertArgs& p, int e) {
+  ExpertSlice q;
+  if (p.xw && e == p.E - 1) {
+    q.w = p.xw; q.w2 = p.xw2; q.ws = p.xws; q.ws2 = p.xws2; q.scale_expert = 0;
+  } else {
+    const int64_t ebase = (int64_t)e * p.N * p.K;
+    q.w = p.w + ebase; q.w2 = p.w2 ? p.w2 + ebase : nullptr; q.ws = p.ws; q.ws2 = p.ws2;
+    q.scale_expert = e;
+  }
+  return q;
 }
 
 // Source row of tile row `idx` of expert e in the activation buffer, clamped
@@ -271,6 +301,8 @@ void expert_tiled_kernel(ExpertArgs p) {
   const int KB = p.K / kBlock, NB = (p.N + kBlock - 1) / kBlock;
   const int kb0 = part * p.kb_per_part, kb1 = kb0 + p.kb_per_part;
 
+  const ExpertSlice xs = expert_slice(p, e);
+
   // Gathered source rows and scatter destinations of this tile.
   for (int i = tid; i < BM; i += THREADS) {
     const int idx = row0 + i;
@@ -289,16 +321,15 @@ void expert_tiled_kernel(ExpertArgs p) {
     for (int i = 0; i < Plan::CA; ++i)
       plan.a_off[i] = (uint32_t)rows_src[row + i * Plan::RSTEP] * (uint32_t)p.K + ch * 16;
     plan.a_base = p.x;
-    const int64_t ebase = (int64_t)e * p.N * p.K;
     if constexpr (PAIRED) {
       // B row rho: 16-row tile j = rho/16 is gate (even j) or up (odd j)
       // column n0 + (rho/32)*16 + rho%16; the parity is fixed per thread.
       const bool up = (row >> 4) & 1;
-      plan.b_base = (up ? p.w2 : p.w) + ebase;
+      plan.b_base = up ? xs.w2 : xs.w;
       plan.b_off = (uint32_t)(n0 + (row >> 5) * 16 + (row & 15)) * (uint32_t)p.K + ch * 16;
       plan.b_step = (uint32_t)(Plan::RSTEP / 2) * (uint32_t)p.K;
     } else {
-      plan.b_base = p.w + ebase;
+      plan.b_base = xs.w;
       plan.b_off = (uint32_t)(n0 + row) * (uint32_t)p.K + ch * 16;
       plan.b_step = (uint32_t)Plan::RSTEP * (uint32_t)p.K;
     }
@@ -310,7 +341,7 @@ void expert_tiled_kernel(ExpertArgs p) {
   const int a_row0 = wm * WM, b_row0 = wn * WN;
   // Scale block of this wave's columns (gate and up share it when paired).
   const int wcol = PAIRED ? n0 + b_row0 / 2 : n0 + b_row0;
-  const int64_t ws_base = ((int64_t)e * NB + wcol / kBlock) * KB;
+  const int64_t ws_base = ((int64_t)xs.scale_expert * NB + wcol / kBlock) * KB;
 
   Acc<MT, NT> acc;
   acc.clear();
@@ -323,8 +354,8 @@ void expert_tiled_kernel(ExpertArgs p) {
     // one stage: stash, prefetch the next k-block, barrier, multiply, barrier
     plan.fetch(kb0, ra, rb);
     ras = as_row[kb0];
-    rws0 = load_scale_t<SDT>(p.ws, ws_base + kb0);
-    if constexpr (PAIRED) rws1 = load_scale_t<SDT>(p.ws2, ws_base + kb0);
+    rws0 = load_scale_t<SDT>(xs.ws, ws_base + kb0);
+    if constexpr (PAIRED) rws1 = load_scale_t<SDT>(xs.ws2, ws_base + kb0);
     for (int kb = kb0; kb < kb1; ++kb) {
       if (kb > kb0) __syncthreads();  // the previous multiply is done with the stage
       plan.stash(lds, ra, rb);
@@ -333,8 +364,8 @@ void expert_tiled_kernel(ExpertArgs p) {
       const int nxt = min(kb + 1, kb1 - 1);
       plan.fetch(nxt, ra, rb);
       ras = as_row[nxt];
-      rws0 = load_scale_t<SDT>(p.ws, ws_base + nxt);
-      if constexpr (PAIRED) rws1 = load_scale_t<SDT>(p.ws2, ws_base + nxt);
+      rws0 = load_scale_t<SDT>(xs.ws, ws_base + nxt);
+      if constexpr (PAIRED) rws1 = load_scale_t<SDT>(xs.ws2, ws_base + nxt);
       __syncthreads();
       mma_stage<MT, NT, PAIRED>(acc, lds, lds + BM * 128, lds_as[0], a_row0, b_row0, ws0, lane, ws1);
     }
@@ -342,16 +373,16 @@ void expert_tiled_kernel(ExpertArgs p) {
   } else {
     plan.fetch(kb0, ra, rb);
     ras = as_row[kb0];
-    float ws0 = load_scale_t<SDT>(p.ws, ws_base + kb0);
-    float ws1 = PAIRED ? load_scale_t<SDT>(p.ws2, ws_base + kb0) : 0.f;
+    float ws0 = load_scale_t<SDT>(xs.ws, ws_base + kb0);
+    float ws1 = PAIRED ? load_scale_t<SDT>(xs.ws2, ws_base + kb0) : 0.f;
     plan.stash(lds, ra, rb);
     if (tid < BM) lds_as[0][tid] = ras;
     {
       const int nxt = min(kb0 + 1, kb1 - 1);
       plan.fetch(nxt, ra, rb);
       ras = as_row[nxt];
-      rws0 = load_scale_t<SDT>(p.ws, ws_base + nxt);
-      if constexpr (PAIRED) rws1 = load_scale_t<SDT>(p.ws2, ws_base + nxt);
+      rws0 = load_scale_t<SDT>(xs.ws, ws_base + nxt);
+      if constexpr (PAIRED) rws1 = load_scale_t<SDT>(xs.ws2, ws_base + nxt);
     }
     __syncthreads();
 
@@ -366,8 +397,8 @@ void expert_tiled_kernel(ExpertArgs p) {
       const int nxt = min(kb + 2, kb1 - 1);
       plan.fetch(nxt, ra, rb);
       ras = as_row[nxt];
-      rws0 = load_scale_t<SDT>(p.ws, ws_base + nxt);
-      if constexpr (PAIRED) rws1 = load_scale_t<SDT>(p.ws2, ws_base + nxt);
+      rws0 = load_scale_t<SDT>(xs.ws, ws_base + nxt);
+      if constexpr (PAIRED) rws1 = load_scale_t<SDT>(xs.ws2, ws_base + nxt);
       __syncthreads();
     }
   }
@@ -518,6 +549,7 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
   const int KB = p.K / kBlock, NB = (p.N + kBlock - 1) / kBlock;
   const int kb0 = part * p.kb_per_part, kb1 = kb0 + p.kb_per_part;
 
+  const ExpertSlice xs = expert_slice(p, e);
   for (int i = tid; i < BM; i += dma::THREADS) {
     const int idx = row0 + i;
     const bool live = idx < count;
@@ -532,9 +564,9 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
   const int nkb = kb1 - kb0;
   for (int i = tid; i < 2 * nkb; i += dma::THREADS) {
     const int h = i / nkb, k = kb0 + i % nkb;
-    const void* src = (PAIRED && h) ? p.ws2 : p.ws;
+    const void* src = (PAIRED && h) ? xs.ws2 : xs.ws;
     const int cb = PAIRED ? n0 / kBlock : min((n0 + 128 * h) / kBlock, NB - 1);
-    const int64_t at = ((int64_t)e * NB + cb) * KB + k;
+    const int64_t at = ((int64_t)xs.scale_expert * NB + cb) * KB + k;
     dma::wtab[h][i % nkb] = p.ws_dtype == AKAS_DTYPE_F32 ? load_scale_t<AKAS_DTYPE_F32>(src, at)
                                                          : load_scale_t<AKAS_DTYPE_BF16>(src, at);
   }
@@ -556,9 +588,8 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
     plan.scales = true;
     plan.skip = row0 + (wave & 3) * 64 >= count;  // a quarter of padding rows only
   } else {
-    const int64_t ebase = (int64_t)e * p.N * p.K;
-    plan.src = p.w + ebase;
-    plan.alt_delta = PAIRED ? (int64_t)(p.w2 - p.w) : 0;
+    plan.src = xs.w;
+    plan.alt_delta = PAIRED ? (int64_t)(xs.w2 - xs.w) : 0;
     plan.alt_mask = PAIRED ? 0xCCu : 0u;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -1082,6 +1113,115 @@ extern "C" int akas_fp8_experts(const void* x, int x_dtype, const uint8_t* w, co
     case AKAS_DTYPE_BF16: launch_partial<AKAS_DTYPE_BF16>(a, s); break;
     default: launch_partial<AKAS_DTYPE_F16>(a, s);
   }
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// The shared-expert MoE block in one call: the shared expert is expert E of
+// the routed launches (rank `top` of every row), so the block is six
+// launches (router, quantize, routes, gate/up + SwiGLU + requant, down,
+// combine) with no dense launches beside them.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct BlockLayout {
+  size_t ids, weights, codes, scales, counts, routes, act, act_scales, contributions, total;
+};
+
+BlockLayout block_layout(int64_t r, int experts, int top, int64_t h, int64_t f) {
+  BlockLayout L{};
+  size_t at = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = at;
+    at += align256(bytes);
+    return o;
+  };
+  const int64_t ranks = r * (top + 1);
+  L.ids = take((size_t)(r * top) * sizeof(int32_t));
+  L.weights = take((size_t)(r * top) * sizeof(float));
+  L.codes = take((size_t)(r * h));
+  L.scales = take((size_t)(r * (h / kBlock)) * sizeof(float));
+  L.counts = take((size_t)(experts + 1) * sizeof(int32_t));
+  L.routes = take((size_t)(experts + 1) * (size_t)r * sizeof(int32_t));
+  L.act = take((size_t)(ranks * f));
+  L.act_scales = take((size_t)(ranks * (f / kBlock)) * sizeof(float));
+  L.contributions = take((size_t)(ranks * h) * sizeof(uint16_t));
+  L.total = at;
+  return L;
+}
+
+}  // namespace
+
+extern "C" size_t akas_shared_expert_moe_workspace_size(int64_t r, int experts, int top, int64_t h,
+                                                        int64_t f) {
+  if (r <= 0 || experts < 1 || top < 1 || h <= 0 || f <= 0) return 0;
+  return block_layout(r, experts, top, h, f).total;
+}
+
+extern "C" int akas_shared_expert_moe(
+    const void* x, int x_dtype, const float* logits, const void* shared_gate, int gate_dtype,
+    const uint8_t* w1, const void* s1, const uint8_t* w3, const void* s3, const uint8_t* w2,
+    const void* s2, const uint8_t* sw1, const void* ss1, const uint8_t* sw3, const void* ss3,
+    const uint8_t* sw2, const void* ss2, int scale_dtype, float* out, void* workspace,
+    size_t workspace_bytes, int64_t r, int experts, int top, int64_t h, int64_t f,
+    void* stream) {
+  if (r < 0 || experts < 1 || experts + 1 > 1024 || top < 1 || top > 32 || top > experts ||
+      h <= 0 || f <= 0 || h % kBlock || f % kBlock || r > 65535 * 64)
+    return AKAS_ERR_GEOMETRY;
+  const int64_t ranks = r * (top + 1);
+  int st = check_common(r, top + 1, experts + 1, f, h, 64, 0, r);
+  if (st == AKAS_OK) st = check_common(r, top + 1, experts + 1, h, f, 64, 0, ranks);
+  if (st != AKAS_OK) return st;
+  if ((uint64_t)(experts + 1) * (uint64_t)r >= (1ull << 31)) return AKAS_ERR_GEOMETRY;
+  if (!float_dtype(x_dtype) || !float_dtype(gate_dtype) || !scale_dtype_ok(scale_dtype))
+    return AKAS_ERR_DTYPE;
+  if (r == 0) return AKAS_OK;
+  if (!x || !logits || !shared_gate || !w1 || !s1 || !w3 || !s3 || !w2 || !s2 || !sw1 || !ss1 ||
+      !sw3 || !ss3 || !sw2 || !ss2 || !out)
+    return AKAS_ERR_NULL;
+  const BlockLayout L = block_layout(r, experts, top, h, f);
+  if (!workspace || workspace_bytes < L.total) return AKAS_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
+    return AKAS_ERR_GEOMETRY;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  uint8_t* base = reinterpret_cast<uint8_t*>(workspace);
+  int32_t* ids = reinterpret_cast<int32_t*>(base + L.ids);
+  float* weights = reinterpret_cast<float*>(base + L.weights);
+  uint8_t* codes = base + L.codes;
+  float* scales = reinterpret_cast<float*>(base + L.scales);
+  int32_t* counts = reinterpret_cast<int32_t*>(base + L.counts);
+  int32_t* routes = reinterpret_cast<int32_t*>(base + L.routes);
+  uint8_t* act = base + L.act;
+  float* act_scales = reinterpret_cast<float*>(base + L.act_scales);
+  uint16_t* contributions = reinterpret_cast<uint16_t*>(base + L.contributions);
+
+  st = launch_decode_router(logits, ids, weights, r, experts, top, s);
+  if (st != AKAS_OK) return st;
+  st = launch_quantize(x, x_dtype, codes, scales, r, h, false, s);
+  if (st != AKAS_OK) return st;
+  launch_routes_with_shared(ids, counts, routes, r, experts, top, s);
+
+  ExpertArgs g{};
+  g.x = codes; g.as = scales; g.w = w1; g.ws = s1; g.w2 = w3; g.ws2 = s3;
+  g.xw = sw1; g.xws = ss1; g.xw2 = sw3; g.xws2 = ss3;
+  g.counts = counts; g.routes = routes; g.out = act; g.out_scales = act_scales;
+  g.r = (int)r; g.top = top + 1; g.E = experts + 1; g.N = (int)f; g.K = (int)h;
+  g.x_rows = (int)r; g.out_rows = (int)ranks;
+  g.parts = 1; g.kb_per_part = (int)(h / kBlock);
+  g.ws_dtype = scale_dtype; g.prod_dtype = AKAS_DTYPE_F32; g.act_dtype = AKAS_DTYPE_F32;
+  launch_swiglu(g, s);
+
+  ExpertArgs d{};
+  d.x = act; d.as = act_scales; d.w = w2; d.ws = s2; d.xw = sw2; d.xws = ss2;
+  d.counts = counts; d.routes = routes; d.out = contributions;
+  d.r = (int)r; d.top = top + 1; d.E = experts + 1; d.N = (int)h; d.K = (int)f;
+  d.routed = 1; d.x_rows = (int)ranks; d.out_rows = (int)ranks;
+  d.parts = 1; d.kb_per_part = (int)(f / kBlock);
+  d.ws_dtype = scale_dtype;
+  launch_partial<AKAS_DTYPE_BF16>(d, s);
+
+  launch_shared_rank_combine(contributions, weights, shared_gate, gate_dtype, out, r, top, h, s);
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }

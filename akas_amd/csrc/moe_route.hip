@@ -6,6 +6,7 @@
 // selection compares IEEE float32 scores with lowest-index tie breaking and
 // the route compaction is an ordered block scan, never an atomic cursor.
 #include "common.h"
+#include "moe_launch.h"
 #include "quant_group.h"
 
 namespace akas {
@@ -291,22 +292,34 @@ __global__ __launch_bounds__(256) void router_quantize_kernel(
 // ---------------------------------------------------------------------------
 // quantized_routes: one 1024-thread workgroup per expert, ordered block scan
 // over the rows (src/akas/ops/moe/kernel.py:121-151, cuda.py:2187-2322)
+//
+// A route names the (row, rank) entry row * ld + rank (ld = top for
+// quantized_routes).  With ld = top + 1, one more workgroup (expert index
+// `experts`) routes every active row at rank top: the shared expert of the
+// shared-expert block, riding in the routed launches.  Null active: every
+// row is active.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void routes_kernel(const int32_t* __restrict__ ids,
                                                       const int32_t* __restrict__ active,
                                                       int32_t* __restrict__ counts,
                                                       int32_t* __restrict__ routes, int64_t rows,
-                                                      int top) {
+                                                      int top, int ld = 0) {
   __shared__ int wave_tot[16];
   const int e = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int32_t* out = routes + (int64_t)e * rows;
+  if (ld == 0) ld = top;
+  const bool extra = e == (int)gridDim.x - 1 && ld > top;  // the rank-`top` expert
   int64_t base = 0;
   for (int64_t r0 = 0; r0 < rows; r0 += 1024) {
     const int64_t row = r0 + tid;
     int cnt = 0;
-    if (row < rows && active[row] != 0) {
-      for (int k = 0; k < top; ++k) cnt += ids[row * top + k] == e;
+    if (row < rows && (!active || active[row] != 0)) {
+      if (extra) {
+        cnt = 1;
+      } else {
+        for (int k = 0; k < top; ++k) cnt += ids[row * top + k] == e;
+      }
     }
     const int incl = wave_inclusive_scan(cnt, lane);
     if (lane == 63) wave_tot[wave] = incl;
@@ -320,11 +333,15 @@ __global__ __launch_bounds__(1024) void routes_kernel(const int32_t* __restrict_
     }
     if (cnt) {
       int64_t pos = base + before + incl - cnt;
-      for (int k = 0; k < top; ++k)
-        if (ids[row * top + k] == e) {
-          if (pos < rows) out[pos] = (int32_t)(row * top + k);
-          ++pos;
-        }
+      if (extra) {
+        if (pos < rows) out[pos] = (int32_t)(row * ld + top);
+      } else {
+        for (int k = 0; k < top; ++k)
+          if (ids[row * top + k] == e) {
+            if (pos < rows) out[pos] = (int32_t)(row * ld + k);
+            ++pos;
+          }
+      }
     }
     base += total;
     __syncthreads();
@@ -592,6 +609,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ e
 // SHARED (moe_combine, src/akas/ops/moe/cuda.py:392-422): each rank's value
 // is rounded to bf16 before its fold, and the shared expert enters as
 // bf16(shared) / (1 + exp(-bf16(gate))) added after the ranks.
+//
+// ld: ranks per row of `experts` (top, or more when further ranks follow the
+// combined ones); shared_ld: elements per row of `shared` (c, or ld * c for a
+// shared expert stored as a rank of `experts`).
 template <int DT, bool SHARED = false>
 __global__ __launch_bounds__(256) void combine8_kernel(const void* __restrict__ experts,
                                                        const float* __restrict__ weights,
@@ -600,7 +621,10 @@ __global__ __launch_bounds__(256) void combine8_kernel(const void* __restrict__ 
                                                        int64_t c, const void* __restrict__ shared = nullptr,
                                                        int shared_dtype = 0,
                                                        const void* __restrict__ gate = nullptr,
-                                                       int gate_dtype = 0) {
+                                                       int gate_dtype = 0, int ld = 0,
+                                                       int64_t shared_ld = 0) {
+  if (ld == 0) ld = top;
+  if (shared_ld == 0) shared_ld = c;
   const int64_t row = blockIdx.y;
   const int64_t col = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
   if (col >= c) return;
@@ -616,7 +640,7 @@ __global__ __launch_bounds__(256) void combine8_kernel(const void* __restrict__ 
       for (int u = 0; u < U; ++u) {
         const int k = min(k0 + u, top - 1);  // unconditional: a clamped rank is never folded
         wv[u] = weights[row * top + k];
-        const int64_t base = (row * top + k) * c + col;
+        const int64_t base = (row * ld + k) * c + col;
         if constexpr (DT == AKAS_DTYPE_F32) {
           const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(experts) + base);
           raw[u][0] = src[0];
@@ -657,7 +681,7 @@ __global__ __launch_bounds__(256) void combine8_kernel(const void* __restrict__ 
     const float den = 1.0f + expf(-g);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      acc[j] += __fdiv_rn(round_bf16(load_elem(shared, row * c + col + j, shared_dtype)), den);
+      acc[j] += __fdiv_rn(round_bf16(load_elem(shared, row * shared_ld + col + j, shared_dtype)), den);
   }
   float4* dst = reinterpret_cast<float4*>(out + row * c + col);
   dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
@@ -711,6 +735,40 @@ static int check_router(const float* logits, int32_t* ids, float* weights, int64
   if (r > 0 && (!logits || !ids || !weights)) return AKAS_ERR_NULL;
   return AKAS_OK;
 }
+
+// Launches of the shared-expert block (akas_shared_expert_moe), declared in
+// moe_launch.h; the arguments are checked by that entry point.
+namespace akas {
+
+int launch_decode_router(const float* logits, int32_t* ids, float* weights, int64_t r,
+                         int experts, int top, hipStream_t s) {
+  const int st = check_router(logits, ids, weights, r, experts, top);
+  if (st != AKAS_OK || r == 0) return st;
+  launch_router<1, 1>(logits, nullptr, ids, weights, r, experts, top, 1.0f, 1, s);
+  return AKAS_OK;
+}
+
+void launch_routes_with_shared(const int32_t* ids, int32_t* counts, int32_t* routes, int64_t r,
+                               int experts, int top, hipStream_t s) {
+  routes_kernel<<<experts + 1, 1024, 0, s>>>(ids, nullptr, counts, routes, r, top, top + 1);
+}
+
+void launch_shared_rank_combine(const uint16_t* contributions, const float* weights,
+                                const void* gate, int gate_dtype, float* out, int64_t r, int top,
+                                int64_t c, hipStream_t s) {
+  const int ld = top + 1;
+  for (int64_t r0 = 0; r0 < r; r0 += 65535) {
+    const int64_t rr = r - r0 < 65535 ? r - r0 : 65535;
+    const uint16_t* ex = contributions + r0 * ld * c;
+    const char* ga = reinterpret_cast<const char*>(gate) + r0 * (gate_dtype == AKAS_DTYPE_F32 ? 4 : 2);
+    dim3 grid((unsigned)((c / 8 + 255) / 256), (unsigned)rr);
+    combine8_kernel<AKAS_DTYPE_BF16, true><<<grid, 256, 0, s>>>(
+        ex, weights + r0 * top, nullptr, out + r0 * c, top, c, ex + (int64_t)top * c,
+        AKAS_DTYPE_BF16, ga, gate_dtype, ld, (int64_t)ld * c);
+  }
+}
+
+}  // namespace akas
 
 extern "C" int akas_biased_router(const float* logits, const float* bias, int32_t* ids,
                                   float* weights, int64_t r, int experts, int top, float scale,

@@ -854,6 +854,64 @@ def moe_combine(experts, weights, shared, gate, *, out=None):
     return out
 
 
+def shared_expert_moe_workspace(r, experts, top, h, f, device):
+    """Workspace of :func:`shared_expert_moe_block` (route tables, x's codes,
+    the activations' codes and the bf16 contributions of top + 1 ranks)."""
+    n = _lib.load().akas_shared_expert_moe_workspace_size(r, experts, top, h, f)
+    return torch.empty(max(int(n), 1), dtype=torch.uint8, device=device)
+
+
+@_on_tensor_device
+def shared_expert_moe_block(x, logits, shared_gate, w1, s1, w3, s3, w2, s2, sw1, ss1, sw3, ss3,
+                            sw2, ss2, *, top, out=None, workspace=None):
+    """The shared-expert MoE block in one call: ``x [r, h]``, router
+    ``logits`` f32 ``[r, E]``, ``shared_gate [r]`` -> f32 ``[r, h]``.
+
+    decode_router (src/akas/ops/moe/cuda.py:2011-2050), the routed experts
+    (bank ``w1``/``w3`` ``[E, f, h]``, ``w2`` ``[E, h, f]``) and the shared
+    expert (``sw1``/``sw3`` ``[f, h]``, ``sw2`` ``[h, f]``) with f32
+    products and activations, and moe_combine with the sigmoid gate
+    (cuda.py:392-422), all six weights' block scales of one dtype.  The
+    shared expert is computed as one more expert of the routed launches.
+    """
+    _need(x, "x", _FLOATS)
+    _need(logits, "logits", torch.float32)
+    if x.dim() != 2 or logits.dim() != 2 or logits.shape[0] != x.shape[0]:
+        raise ValueError("shared_expert_moe_block expects x [r, h] and logits [r, E]")
+    r, h = x.shape
+    experts = logits.shape[1]
+    _need(shared_gate, "shared_gate", _FLOATS)
+    if shared_gate.numel() != r or shared_gate.dim() > 2:
+        raise ValueError("shared_gate must be [r] or [r, 1]")
+    _need(w1, "w1", torch.uint8)
+    if w1.dim() != 3 or w1.shape[0] != experts or w1.shape[2] != h:
+        raise ValueError("w1 must be [E, f, h]")
+    f = w1.shape[1]
+    if h % BLOCK or f % BLOCK:
+        raise ValueError("shared_expert_moe_block widths must be multiples of 128")
+    _need(w3, "w3", torch.uint8, (experts, f, h))
+    _need(w2, "w2", torch.uint8, (experts, h, f))
+    _need(s1, "s1", _SCALES, (experts, f // BLOCK, h // BLOCK))
+    _need(s3, "s3", s1.dtype, (experts, f // BLOCK, h // BLOCK))
+    _need(s2, "s2", s1.dtype, (experts, h // BLOCK, f // BLOCK))
+    _need(sw1, "sw1", torch.uint8, (f, h))
+    _need(sw3, "sw3", torch.uint8, (f, h))
+    _need(sw2, "sw2", torch.uint8, (h, f))
+    _need(ss1, "ss1", s1.dtype, (f // BLOCK, h // BLOCK))
+    _need(ss3, "ss3", s1.dtype, (f // BLOCK, h // BLOCK))
+    _need(ss2, "ss2", s1.dtype, (h // BLOCK, f // BLOCK))
+    out = _out(out, "out", (r, h), torch.float32, x)
+    if workspace is None:
+        workspace = shared_expert_moe_workspace(r, experts, top, h, f, x.device)
+    _need(workspace, "workspace", torch.uint8)
+    check(_lib.load().akas_shared_expert_moe(
+        _ptr(x), _dt(x.dtype), _ptr(logits), _ptr(shared_gate), _dt(shared_gate.dtype),
+        _ptr(w1), _ptr(s1), _ptr(w3), _ptr(s3), _ptr(w2), _ptr(s2), _ptr(sw1), _ptr(ss1),
+        _ptr(sw3), _ptr(ss3), _ptr(sw2), _ptr(ss2), _dt(s1.dtype), _ptr(out), _ptr(workspace),
+        workspace.numel(), r, experts, top, h, f, _stream()), "shared_expert_moe")
+    return out
+
+
 @_on_tensor_device
 def routed_combine(experts, weights, active, *, out=None):
     """``routed_combine(r, top, c[, input_dtype]): experts, weights, active -> out``.

@@ -460,6 +460,36 @@ int akas_routed_combine(const void* experts, int input_dtype, const float* weigh
                         const int32_t* active, float* out, int64_t r, int top, int64_t c,
                         void* stream);
 
+/*
+ * The shared-expert MoE block (Qwen3.5 block-fp8) in one call:
+ * x f32/f16/bf16 [r, h], router logits f32 [r, experts] and the shared
+ * expert's gate logit shared_gate f32/f16/bf16 [r] -> out f32 [r, h].
+ * No counterpart in the reference, whose program composes the block from
+ * kinds (src/akas/ops/moe/definition.py:293-418): decode_router
+ * (cuda.py:2011-2050), quantize, the routed experts' gate/up, SwiGLU, FP8
+ * re-quantization and down products (f32 products and activations), the
+ * shared expert's FP8 gate/up -> SwiGLU -> FP8 down as dense linears, and
+ * moe_combine (cuda.py:392-422).  For callers that run the whole block: the
+ * shared expert (sw1/sw3 [f, h], sw2 [h, f], scales as the bank's) is
+ * computed as expert `experts` of the routed launches, at rank top of every
+ * row, so the block takes six launches and no dense launches beside them.
+ * Bank w1/w3 [experts, f, h], w2 [experts, h, f], 128x128 block scales of
+ * scale_dtype (f32 or bf16) for all six weights.  Contributions are kept in
+ * bf16, which moe_combine rounds them to.  h % 128 == 0, f % 128 == 0,
+ * experts + 1 <= 1024, top <= 32; workspace (16-byte aligned) of at least
+ * akas_shared_expert_moe_workspace_size() bytes; out 16-byte aligned.
+ */
+size_t akas_shared_expert_moe_workspace_size(int64_t r, int experts, int top, int64_t h,
+                                             int64_t f);
+int akas_shared_expert_moe(const void* x, int x_dtype, const float* logits,
+                           const void* shared_gate, int gate_dtype, const uint8_t* w1,
+                           const void* s1, const uint8_t* w3, const void* s3, const uint8_t* w2,
+                           const void* s2, const uint8_t* sw1, const void* ss1,
+                           const uint8_t* sw3, const void* ss3, const uint8_t* sw2,
+                           const void* ss2, int scale_dtype, float* out, void* workspace,
+                           size_t workspace_bytes, int64_t r, int experts, int top, int64_t h,
+                           int64_t f, void* stream);
+
 #if defined(__GNUC__)
 #pragma GCC visibility pop
 #endif

@@ -87,10 +87,28 @@ def test_host_validation_rejects_before_launch():
     # fused swiglu: packed output without packed input
     assert lib.akas_fp8_expert_swiglu(1, 1, 1, 1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 4, 2, 4, 128,
                                       256, 0, 0, 64, 0, 1, None) == -1
+    # shared-expert block: 1024 experts leave no index for the shared one, h
+    # not a multiple of 128, gate dtype code, nulls, workspace, no rows
+    blk = lambda x, gdt, ws, wsb, r, e, top, h, f: lib.akas_shared_expert_moe(
+        x, 2, 1, 1, gdt, *([1] * 12), 0, 16, ws, wsb, r, e, top, h, f, None)
+    assert blk(1, 0, 16, big, 4, 1024, 8, 256, 128) == -1
+    assert blk(1, 0, 16, big, 4, 32, 8, 200, 128) == -1
+    assert blk(1, 0, 16, big, 4, 32, 33, 256, 128) == -1
+    assert blk(1, 9, 16, big, 4, 32, 8, 256, 128) == -3
+    assert blk(None, 0, 16, big, 4, 32, 8, 256, 128) == -2
+    assert blk(1, 0, 16, 64, 4, 32, 8, 256, 128) == -5
+    assert blk(1, 0, None, big, 4, 32, 8, 256, 128) == -5
+    assert blk(None, 0, None, 0, 0, 32, 8, 256, 128) == 0
 
 
 def test_workspace_size_formula():
     lib = _lib.load()
+    # shared-expert block, 4 rows, 8 experts, top 2, h 256, f 128: ids and
+    # weights, x's codes and scales, counts, routes, then 12 ranks' activation
+    # codes, scales and bf16 contributions, each 256-byte aligned
+    assert lib.akas_shared_expert_moe_workspace_size(4, 8, 2, 256, 128) == (
+        256 + 256 + 1024 + 256 + 256 + 256 + 1536 + 256 + 6144)
+    assert lib.akas_shared_expert_moe_workspace_size(0, 8, 2, 256, 128) == 0
     assert lib.akas_fp8_linear_workspace_size(16, 2048, 6144) == 16 * 2048 + 16 * 16 * 4
     assert lib.akas_fp8_linear_workspace_size(0, 2048, 6144) == 0
     # codes take whole 16-row tiles (the decode GEMM's fragment-major layout)

@@ -1298,10 +1298,84 @@ def test_shared_expert_moe_block_group_kinds(dev, rows, E, H, F):
     assert rel_fro(out, ref_path) < 1e-3
 
 
-def test_shared_expert_moe_block_graph_replays(dev):
-    """The block forks the shared expert onto a second stream and joins it
-    before the combine; captured in a HIP graph, every replay (with eager work
-    and synchronizations between them) equals the eager result."""
+@pytest.mark.parametrize("rows,E,H,F,top,x_dtype,scale_dtype,gate_dtype", [
+    (6, 32, 256, 128, 8, "bfloat16", "float32", "float32"),     # 32-row decode tiles
+    (64, 256, 2048, 512, 8, "bfloat16", "bfloat16", "float32"),  # the Qwen3.5 decode batch
+    (1, 8, 256, 128, 1, "float32", "float32", "bfloat16"),      # one row, top 1
+    (300, 32, 256, 256, 8, "float16", "float32", "float32"),    # 128-row tiles
+    (1024, 16, 512, 256, 8, "bfloat16", "float32", "bfloat16"),  # DMA-fed 256-row tiles
+    (97, 64, 384, 384, 4, "bfloat16", "bfloat16", "float16")])
+def test_shared_expert_block_is_its_kinds(dev, rows, E, H, F, top, x_dtype, scale_dtype,
+                                          gate_dtype):
+    """The one-call block equals, bit for bit, the kinds it fuses run one by
+    one over a bank extended with the shared expert as expert E: router ->
+    quantize -> quantized_routes over ids with rank `top` = E on every row ->
+    fp8_expert_swiglu -> expert_partial (bf16) -> moe_combine with rank
+    `top` as the shared expert.  The row tiles of the grouped kernels differ
+    with the rows per expert (decode, 128-row, DMA-fed)."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(rows * 7 + E)
+    sdt = getattr(torch, scale_dtype)
+    g = torch.Generator(device=dev)
+    g.manual_seed(rows + E)
+    bank = {}
+    for name, shape in (("w1", (E, F, H)), ("w3", (E, F, H)), ("w2", (E, H, F)),
+                        ("sw1", (F, H)), ("sw3", (F, H)), ("sw2", (H, F))):
+        w = torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * 0.05
+        bank[name] = ops.quantize_weight_blocks(w, scale_dtype=sdt)
+    x = _t(bf16_normal(rng, (rows, H)), dev, getattr(torch, x_dtype))
+    logits = _t(rng.normal(0, 1, (rows, E)).astype(np.float32), dev)
+    gate = _t(rng.normal(0, 1.5, rows).astype(np.float32), dev, getattr(torch, gate_dtype))
+    args = [t for n in ("w1", "w3", "w2", "sw1", "sw3", "sw2") for t in bank[n]]
+    out = ops.shared_expert_moe_block(x, logits, gate, *args, top=top)
+
+    ids, prob = ops.router(logits, top=top)
+    codes, scales = ops.quantize(x)
+    ext = torch.cat([ids, torch.full((rows, 1), E, dtype=torch.int32, device=dev)], 1).contiguous()
+    counts, routes = ops.quantized_routes(ext, torch.ones(rows, dtype=torch.int32, device=dev),
+                                          experts=E + 1)
+    full = {n: tuple(torch.cat([bank[n][i], bank["s" + n][i].unsqueeze(0)]).contiguous()
+                     for i in range(2)) for n in ("w1", "w3", "w2")}
+    act, act_scales = ops.fp8_expert_swiglu(codes, scales, *full["w1"], *full["w3"], counts, routes,
+                                            r=rows, top=top + 1)
+    contrib = ops.expert_partial(act, act_scales, *full["w2"], counts, routes, r=rows, top=top + 1,
+                                 routed_input=True, output_dtype=torch.bfloat16)
+    want = ops.moe_combine(contrib[:, :top].contiguous(), prob, contrib[:, top].contiguous(), gate)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_np(out), _np(want))
+    assert np.isfinite(_np(out)).all()
+
+
+def test_shared_expert_block_paths_agree(dev):
+    """The shared expert on a second stream (dense FP8 linears) and as an
+    expert of the routed launches give the same block within the products'
+    summation-order tolerance, at the Qwen3.5 decode size."""
+    import torch
+    from akas_amd import moe
+
+    rows, E, H, F, top = 64, 256, 2048, 512, 8
+    rng = np.random.default_rng(123)
+    dbank, _ = _device_bank(dev, 123, {
+        "w1": (E, F, H), "w3": (E, F, H), "w2": (E, H, F),
+        "sw1": (F, H), "sw3": (F, H), "sw2": (H, F)}, 0.02)
+    wts = moe.ExpertWeights(*(a for n in ("w1", "w3", "w2") for a in dbank[n]))
+    shared = moe.SharedExpert(*(a for n in ("sw1", "sw3", "sw2") for a in dbank[n]))
+    args = (_t(bf16_normal(rng, (rows, H)), dev, torch.bfloat16),
+            _t(rng.normal(0, 1, (rows, E)).astype(np.float32), dev),
+            _t(rng.normal(0, 1.5, rows).astype(np.float32), dev), wts, shared)
+    one_call = _np(moe.shared_expert_moe(*args, top=top))
+    two_streams = _np(moe.shared_expert_moe(*args, top=top, shared_as_expert=False))
+    assert rel_fro(one_call, two_streams) < 1e-4
+
+
+@pytest.mark.parametrize("shared_as_expert", [True, False])
+def test_shared_expert_moe_block_graph_replays(dev, shared_as_expert):
+    """The block captured in a HIP graph, either as one call or with the
+    shared expert forked onto a second stream and joined before the combine:
+    every replay (with eager work and synchronizations between them) equals
+    the eager result."""
     import torch
     from akas_amd import moe
 
@@ -1315,22 +1389,23 @@ def test_shared_expert_moe_block_graph_replays(dev):
     x = _t(bf16_normal(rng, (rows, H)), dev, torch.bfloat16)
     logits = _t(rng.normal(0, 1, (rows, E)).astype(np.float32), dev)
     gate = _t(rng.normal(0, 1.5, rows).astype(np.float32), dev)
-    eager = moe.shared_expert_moe(x, logits, gate, wts, shared, top=top).clone()
+    kw = dict(top=top, shared_as_expert=shared_as_expert)
+    eager = moe.shared_expert_moe(x, logits, gate, wts, shared, **kw).clone()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        moe.shared_expert_moe(x, logits, gate, wts, shared, top=top)
+        moe.shared_expert_moe(x, logits, gate, wts, shared, **kw)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        out = moe.shared_expert_moe(x, logits, gate, wts, shared, top=top)
+        out = moe.shared_expert_moe(x, logits, gate, wts, shared, **kw)
     for _ in range(3):
         out.zero_()
         g.replay()
         torch.cuda.synchronize()
         np.testing.assert_array_equal(_np(out), _np(eager))
-        moe.shared_expert_moe(x, logits, gate, wts, shared, top=top)  # eager work between
+        moe.shared_expert_moe(x, logits, gate, wts, shared, **kw)  # eager work between
         torch.cuda.synchronize()
 
 
