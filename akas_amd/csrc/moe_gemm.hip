@@ -60,6 +60,7 @@ struct ExpertArgs {
   int parts, kb_per_part;
   int ws_dtype, prod_dtype, act_dtype;
   int max_tiles, tiles_n;
+  int fair;  // progress-ordered wave priority in the k-loop (see expert_tiled_kernel)
 };
 
 // Row tiles over all experts (the live part of the tile list); every lane
@@ -249,6 +250,28 @@ AKAS_DEV void combine_tail(const ExpertArgs& p, const int* rows_dst, int* taken,
   }
 }
 
+// Wave priority by the share of its k range a wave has done: 3 in the first
+// quarter down to 0 in the last.  When all of a launch's workgroups are
+// resident at once (one round, several per CU), the SIMDs otherwise favour
+// the oldest workgroup's waves: of the three gate/up workgroups on a CU the
+// first finished 20 us before the last (LFM2 decode layer, 768 workgroups),
+// and the last ran its tail alone at a fraction of the CU's load rate.  A
+// wave that lags keeps the higher priority until it has caught up to within
+// a quarter (per-CU spread 20 -> 5 us, layer 134.0 -> 131.1 us).  With more
+// workgroups than slots the oldest-first order is the better one: finished
+// workgroups free their slots for the next ones.
+AKAS_DEV void wave_priority_by_progress(int done, int total) {
+  const int q = (done * 4) / total;  // wave-uniform
+  if (q == 0)
+    __builtin_amdgcn_s_setprio(3);
+  else if (q == 1)
+    __builtin_amdgcn_s_setprio(2);
+  else if (q == 2)
+    __builtin_amdgcn_s_setprio(1);
+  else
+    __builtin_amdgcn_s_setprio(0);
+}
+
 // STAGES: LDS stages (0: one for the 32-row expert partial, two otherwise).
 // The one-stage paired 32-row tile keeps its registers within three waves per
 // SIMD, so that three workgroups share a CU.
@@ -357,6 +380,8 @@ void expert_tiled_kernel(ExpertArgs p) {
     rws0 = load_scale_t<SDT>(xs.ws, ws_base + kb0);
     if constexpr (PAIRED) rws1 = load_scale_t<SDT>(xs.ws2, ws_base + kb0);
     for (int kb = kb0; kb < kb1; ++kb) {
+      if constexpr (STAGES == 1)
+        if (p.fair) wave_priority_by_progress(kb - kb0, kb1 - kb0);
       if (kb > kb0) __syncthreads();  // the previous multiply is done with the stage
       plan.stash(lds, ra, rb);
       if (tid < BM) lds_as[0][tid] = ras;
@@ -824,9 +849,12 @@ static void launch_paired(const ExpertArgs& a, hipStream_t s) {
   // 135.5 us); when they do not, the two-stage tile's faster workgroups win
   // (Qwen3.5 block, about 900 workgroups: 184.0 against 191.4 us one-stage).
   const int64_t decode_tiles = std::min<int64_t>(a.E, (int64_t)a.r * a.top) * (a.N / 128) * a.parts;
-  if (mean <= 48 && decode_tiles <= 3 * (int64_t)device_cus())
-    launch_expert<32, 256, 1, 4, MODE, OUT, 1>(a, s);
-  else if (mean <= 48)
+  if (mean <= 48 && decode_tiles <= 3 * (int64_t)device_cus()) {
+    // one round: progress-ordered priority once workgroups share CUs
+    ExpertArgs b = a;
+    b.fair = decode_tiles >= 2 * (int64_t)device_cus();
+    launch_expert<32, 256, 1, 4, MODE, OUT, 1>(b, s);
+  } else if (mean <= 48)
     launch_expert<32, 256, 1, 4, MODE, OUT>(a, s);
   else if (aligned && expert_dma_fits(a, mean, dma::BN / 2))
     launch_expert_dma<MODE, OUT>(a, s);
