@@ -63,50 +63,69 @@ struct ExpertArgs {
   int fair;  // progress-ordered wave priority in the k-loop (see expert_tiled_kernel)
 };
 
-// Row tiles over all experts (the live part of the tile list); every lane
-// returns the same total.  Same tile count per expert as locate_tile.
-AKAS_DEV int live_tiles(const int32_t* counts, int experts, int bm, int lane) {
+// The work item of this workgroup: column block nb of row tile `tile` of
+// expert `expert`, whose routed rows number `count` (counts[expert] capped at
+// r).  Items are enumerated over the live row tiles only, column block
+// fastest, before the XCD remap: the grid is sized for the most tiles the
+// routes can produce, and a remap over the whole grid left the dead tail --
+// up to a quarter of the grid -- on the last XCDs, idling them.
+struct Item {
+  int nb, expert, tile, count;
+};
+
+// Position of logical tile t among the row tiles n (one expert per lane) of
+// experts e0 .. e0+63, whose tiles start at `base`: sets the item and
+// returns true when t falls among them, else advances base.
+AKAS_DEV bool tile_in_chunk(int n, int c, int e0, int t, int r, int lane, int& base, Item& it) {
+  const int incl = wave_inclusive_scan(n, lane);
+  const int excl = incl - n;
+  const uint64_t hit = __ballot(t >= base + excl && t < base + incl);
+  if (hit) {
+    const int src = __builtin_ctzll(hit);
+    it.expert = e0 + src;
+    it.tile = t - base - __shfl(excl, src, 64);
+    it.count = min(__shfl(c, src, 64), r);
+    return true;
+  }
+  base += __shfl(incl, 63, 64);
+  return false;
+}
+
+// Returns false for a workgroup past the live items (uniform).  Up to 64
+// experts, counts is read once and the total and the search share those
+// registers: one memory round trip, where separate passes and the count read
+// again after them took three in series.  More experts read counts once per
+// pass, 64 at a time.
+AKAS_DEV bool find_item(const int32_t* counts, int experts, int r, int bm, int tiles_n, int lane,
+                        Item& it) {
+  if (experts <= 64) {
+    const int c = lane < experts ? max(counts[lane], 0) : 0;
+    const int n = (c + bm - 1) / bm;
+    const int items = wave_sum_i(n) * tiles_n;
+    const int id = xcd_remap(blockIdx.x, items);
+    if (id >= items) return false;
+    it.nb = id % tiles_n;
+    int base = 0;
+    return tile_in_chunk(n, c, 0, id / tiles_n, r, lane, base, it);
+  }
   int total = 0;
   for (int e0 = 0; e0 < experts; e0 += 64) {
     const int e = e0 + lane;
-    const int c = e < experts ? counts[e] : 0;
-    total += wave_sum_i(((c > 0 ? c : 0) + bm - 1) / bm);
+    const int c = e < experts ? max(counts[e], 0) : 0;
+    total += wave_sum_i((c + bm - 1) / bm);
   }
-  return total;
-}
-
-// Work item of this workgroup among the live ones.  The grid is sized for the
-// most tiles the routes can produce; enumerating only the live items before
-// the XCD remap spreads them evenly over the eight XCDs (a remap over the
-// whole grid left the dead tail -- up to a quarter of the grid -- on the last
-// XCDs, idling them).  Returns -1 for a workgroup past the live items.
-AKAS_DEV int live_item(const int32_t* counts, int experts, int bm, int tiles_n, int lane) {
-  const int total = live_tiles(counts, experts, bm, lane) * tiles_n;
-  const int id = xcd_remap(blockIdx.x, total);
-  return id < total ? id : -1;
-}
-
-// (expert, tile) of logical tile t; expert = -1 when t is past the last tile.
-AKAS_DEV void locate_tile(const int32_t* counts, int experts, int bm, int t, int lane,
-                          int& expert, int& tile) {
+  const int items = total * tiles_n;
+  const int id = xcd_remap(blockIdx.x, items);
+  if (id >= items) return false;
+  it.nb = id % tiles_n;
+  const int t = id / tiles_n;
   int base = 0;
-  expert = -1;
-  tile = 0;
   for (int e0 = 0; e0 < experts; e0 += 64) {
     const int e = e0 + lane;
-    const int c = e < experts ? counts[e] : 0;
-    const int n = ((c > 0 ? c : 0) + bm - 1) / bm;
-    const int incl = wave_inclusive_scan(n, lane);
-    const int excl = incl - n;
-    const uint64_t hit = __ballot(t >= base + excl && t < base + incl);
-    if (hit) {
-      const int src = __builtin_ctzll(hit);
-      expert = e0 + src;
-      tile = t - base - __shfl(excl, src, 64);
-      return;
-    }
-    base += __shfl(incl, 63, 64);
+    const int c = e < experts ? max(counts[e], 0) : 0;
+    if (tile_in_chunk((c + bm - 1) / bm, c, e0, t, r, lane, base, it)) return true;
   }
+  return false;  // not reached: t < total
 }
 
 // Codes and block scales of expert e: the bank's slice, or the expert kept
@@ -131,17 +150,18 @@ AKAS_DEV ExpertSlice expert_slice(const ExpertArgs& p, int e) {
   return q;
 }
 
-// Source row of tile row `idx` of expert e in the activation buffer, clamped
-// into the buffer (a corrupt route can only misroute, never fault).
-AKAS_DEV int source_row(const ExpertArgs& p, int e, int idx) {
-  int row;
-  if (p.packed_in) {
-    row = p.offsets[e] + idx;
-  } else {
-    const int route = p.routes[(int64_t)e * p.r + idx];
-    row = p.routed ? route : route / p.top;
-  }
-  return row < 0 ? 0 : (row >= p.x_rows ? p.x_rows - 1 : row);
+// Tile row `idx` of expert e (a position below its count): its source row
+// in the activation buffer, clamped into the buffer (a corrupt route can
+// only misroute, never fault), and, when `live`, its scatter destination
+// (else -1).  The route is read once for both.
+AKAS_DEV void tile_row(const ExpertArgs& p, int e, int idx, bool live, int& src, int& dst) {
+  int route = 0, off = 0;
+  if (!p.packed_in || !p.packed_out) route = p.routes[(int64_t)e * p.r + idx];
+  if (p.packed_in || p.packed_out) off = p.offsets[e];
+  const int row = p.packed_in ? off + idx : (p.routed ? route : route / p.top);
+  src = row < 0 ? 0 : (row >= p.x_rows ? p.x_rows - 1 : row);
+  const int d = live ? (p.packed_out ? off + idx : route) : -1;
+  dst = d < p.out_rows ? d : -1;
 }
 
 // Epilogue modes of the grouped kernels.  Modes 1-3 share the paired tile:
@@ -310,13 +330,9 @@ void expert_tiled_kernel(ExpertArgs p) {
   // neighbouring workgroups read one expert's consecutive weight rows and
   // share its activation rows (LFM2 decode layer 145.5 -> 142.6 us, Qwen3.5
   // block 190.5 -> 183.2 us against tiles fastest over the whole grid).
-  const int id = live_item(p.counts, p.E, BM, p.tiles_n, lane);
-  if (id < 0) return;  // past the live items (uniform)
-  const int nb = id % p.tiles_n, t = id / p.tiles_n;
-  int e, tile;
-  locate_tile(p.counts, p.E, BM, t, lane, e, tile);
-  if (e < 0) return;  // uniform across the workgroup
-  const int count = min(p.counts[e], p.r);
+  Item item;
+  if (!find_item(p.counts, p.E, p.r, BM, p.tiles_n, lane, item)) return;  // uniform
+  const int nb = item.nb, e = item.expert, tile = item.tile, count = item.count;
   const int row0 = tile * BM;
   if (row0 >= count) return;  // only reachable with counts[e] > r
   const int n0 = nb * (PAIRED ? BN / 2 : BN);
@@ -330,10 +346,7 @@ void expert_tiled_kernel(ExpertArgs p) {
   for (int i = tid; i < BM; i += THREADS) {
     const int idx = row0 + i;
     const bool live = idx < count;
-    rows_src[i] = source_row(p, e, live ? idx : row0);
-    int dst = -1;
-    if (live) dst = p.packed_out ? p.offsets[e] + idx : p.routes[(int64_t)e * p.r + idx];
-    rows_dst[i] = dst < p.out_rows ? dst : -1;
+    tile_row(p, e, live ? idx : row0, live, rows_src[i], rows_dst[i]);
   }
   __syncthreads();
 
@@ -560,13 +573,9 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   if constexpr (MODE == kCombine) zero_unrouted_rows<dma::THREADS>(p);
-  const int id = live_item(p.counts, p.E, BM, p.tiles_n, lane);
-  if (id < 0) return;  // past the live items (uniform)
-  const int nb = id % p.tiles_n, t = id / p.tiles_n;
-  int e, tile;
-  locate_tile(p.counts, p.E, BM, t, lane, e, tile);
-  if (e < 0) return;  // uniform across the workgroup
-  const int count = min(p.counts[e], p.r);
+  Item item;
+  if (!find_item(p.counts, p.E, p.r, BM, p.tiles_n, lane, item)) return;  // uniform
+  const int nb = item.nb, e = item.expert, tile = item.tile, count = item.count;
   const int row0 = tile * BM;
   if (row0 >= count) return;  // only reachable with counts[e] > r
   const int n0 = nb * (PAIRED ? dma::BN / 2 : dma::BN);
@@ -575,26 +584,35 @@ __global__ __launch_bounds__(dma::THREADS) void expert_dma_kernel(ExpertArgs p) 
   const int kb0 = part * p.kb_per_part, kb1 = kb0 + p.kb_per_part;
 
   const ExpertSlice xs = expert_slice(p, e);
-  for (int i = tid; i < BM; i += dma::THREADS) {
-    const int idx = row0 + i;
-    const bool live = idx < count;
-    rows_src[i] = source_row(p, e, live ? idx : row0);
-    int dst = -1;
-    if (live) dst = p.packed_out ? p.offsets[e] + idx : p.routes[(int64_t)e * p.r + idx];
-    rows_dst[i] = dst < p.out_rows ? dst : -1;
-  }
   // Weight scales over the k range as float32 (either scale dtype gives the
   // same main loop): PAIRED, gate (h = 0) and up (h = 1) of the tile's one
-  // 128-column block; else the tile's two column blocks.
+  // 128-column block; else the tile's two column blocks.  One scale and one
+  // tile row per thread; every load is issued before the first LDS store,
+  // so the scales and the routes take one memory round trip together.
+  static_assert(BM <= dma::THREADS && 2 * dma::MAX_KB <= dma::THREADS, "one entry per thread");
+  // (The scale's raw bits are widened only after the route loads are out.)
   const int nkb = kb1 - kb0;
-  for (int i = tid; i < 2 * nkb; i += dma::THREADS) {
-    const int h = i / nkb, k = kb0 + i % nkb;
+  uint32_t wraw = 0;
+  if (tid < 2 * nkb) {
+    const int h = tid / nkb, k = kb0 + tid % nkb;
     const void* src = (PAIRED && h) ? xs.ws2 : xs.ws;
     const int cb = PAIRED ? n0 / kBlock : min((n0 + 128 * h) / kBlock, NB - 1);
     const int64_t at = ((int64_t)xs.scale_expert * NB + cb) * KB + k;
-    dma::wtab[h][i % nkb] = p.ws_dtype == AKAS_DTYPE_F32 ? load_scale_t<AKAS_DTYPE_F32>(src, at)
-                                                         : load_scale_t<AKAS_DTYPE_BF16>(src, at);
+    wraw = p.ws_dtype == AKAS_DTYPE_F32 ? reinterpret_cast<const uint32_t*>(src)[at]
+                                        : reinterpret_cast<const uint16_t*>(src)[at];
   }
+  int src_row = 0, dst_row = -1;
+  if (tid < BM) {
+    const int idx = row0 + tid;
+    const bool live = idx < count;
+    tile_row(p, e, live ? idx : row0, live, src_row, dst_row);
+  }
+  if (tid < BM) {
+    rows_src[tid] = src_row;
+    rows_dst[tid] = dst_row;
+  }
+  if (tid < 2 * nkb)
+    dma::wtab[tid / nkb][tid % nkb] = __uint_as_float(p.ws_dtype == AKAS_DTYPE_F32 ? wraw : wraw << 16);
   __syncthreads();
 
   dma::GatherPlan plan;
