@@ -21,10 +21,12 @@ template <int CTRL>
 AKAS_DEV void argmax_step(float& s, int& idx) {
   const float os = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), CTRL, 0xF, 0xF, true));
   const int oi = __builtin_amdgcn_update_dpp(0, idx, CTRL, 0xF, 0xF, true);
-  if (os > s || (os == s && oi < idx)) {
-    s = os;
-    idx = oi;
-  }
+  // Selects over non-short-circuit tests: an if, or || and &&, compiled
+  // to exec-mask branches that made each rank of the top-k several times
+  // longer.
+  const bool take = (os > s) | ((os == s) & (oi < idx));
+  s = take ? os : s;
+  idx = take ? oi : idx;
 }
 
 // Arg-max over a 16-lane DPP row: quad swaps, then half-row and row mirrors.
@@ -45,10 +47,9 @@ AKAS_DEV void wave_argmax(float& s, int& idx) {
   for (int r = 1; r < 4; ++r) {
     const float os = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 16 * r));
     const int oi = __builtin_amdgcn_readlane(idx, 16 * r);
-    if (os > bs || (os == bs && oi < bi)) {
-      bs = os;
-      bi = oi;
-    }
+    const bool take = (os > bs) | ((os == bs) & (oi < bi));
+    bs = take ? os : bs;
+    bi = take ? oi : bi;
   }
   s = bs;
   idx = bi;
@@ -84,42 +85,54 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ l
   const float* l = logits + row * experts;
   // base: the value a chosen expert contributes (the logit, or its sigmoid);
   // score: base + bias, the selection key.
-  float base[SLOTS], score[SLOTS];
+  //
+  // Every slot's logit (and bias) load goes out before the first is used:
+  // loads under a per-lane condition each waited for the one before (four
+  // memory round trips in series at 256 experts).  Indices past the experts
+  // read the last one and are masked below.
+  float base[SLOTS], score[SLOTS], raw[SLOTS], braw[SLOTS];
   const int slots = (experts + 63) / 64;
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    const int e = min(s * 64 + lane, experts - 1);
+    raw[s] = l[e];
+    braw[s] = bias ? bias[e] : 0.f;
+  }
 #pragma unroll
   for (int s = 0; s < SLOTS; ++s) {
     const int e = s * 64 + lane;
     float v = 0.f, sc = -__builtin_inff();
     if (s < slots && e < experts) {
-      v = SOFTMAX ? (BF16 ? round_bf16(l[e]) : l[e]) : router_sigmoid(l[e]);
-      sc = v + (bias ? bias[e] : 0.f);
+      v = SOFTMAX ? (BF16 ? round_bf16(raw[s]) : raw[s]) : router_sigmoid(raw[s]);
+      sc = v + braw[s];
     }
     base[s] = v;
     score[s] = sc;
   }
+  bool valid[SLOTS];
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) valid[s] = (s < slots) & (s * 64 + lane < experts);
   float mine = 0.f;
   int mine_id = 0;
   for (int rank = 0; rank < top; ++rank) {
     float best = -__builtin_inff();
     int bi = 0x7FFFFFFF;
-    // slots ascend in expert index, so strict > keeps the lowest index on ties
+    // slots ascend in expert index, so strict > keeps the lowest index on
+    // ties (selects over non-short-circuit tests, as in argmax_step)
 #pragma unroll
     for (int s = 0; s < SLOTS; ++s) {
-      const int e = s * 64 + lane;
-      if (s < slots && e < experts && (score[s] > best || bi == 0x7FFFFFFF)) {
-        best = score[s];
-        bi = e;
-      }
+      const bool take = valid[s] & ((score[s] > best) | (bi == 0x7FFFFFFF));
+      best = take ? score[s] : best;
+      bi = take ? s * 64 + lane : bi;
     }
     wave_argmax(best, bi);
     const int owner = bi & 63, slot = bi >> 6;  // uniform
     float v = 0.f;
 #pragma unroll
-    for (int s = 0; s < SLOTS; ++s)
-      if (s == slot) {
-        v = base[s];
-        if (lane == owner) score[s] = -__builtin_inff();
-      }
+    for (int s = 0; s < SLOTS; ++s) {
+      v = s == slot ? base[s] : v;
+      score[s] = ((s == slot) & (lane == owner)) ? -__builtin_inff() : score[s];
+    }
     v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), owner));
     if (lane == rank) {
       mine = v;
@@ -168,14 +181,21 @@ AKAS_DEV void router_row16(const float* __restrict__ logits, const float* __rest
   const float* lg = logits + (live ? row : 0) * experts;  // spare rows read row 0, never stored
   // base: the value a chosen expert contributes (the logit, or its sigmoid);
   // score: base + bias, the selection key.
-  float base[4], score[4];
+  // (All four loads go out before the first is used, as in router_kernel.)
+  float base[4], score[4], raw[4], braw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = min(l * 4 + i, experts - 1);
+    raw[i] = lg[e];
+    braw[i] = bias ? bias[e] : 0.f;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = l * 4 + i;
     float v = 0.f, sc = -__builtin_inff();
     if (e < experts) {
-      v = SOFTMAX ? (BF16 ? round_bf16(lg[e]) : lg[e]) : router_sigmoid(lg[e]);
-      sc = v + (bias ? bias[e] : 0.f);
+      v = SOFTMAX ? (BF16 ? round_bf16(raw[i]) : raw[i]) : router_sigmoid(raw[i]);
+      sc = v + braw[i];
     }
     base[i] = v;
     score[i] = sc;
@@ -190,23 +210,23 @@ AKAS_DEV void router_row16(const float* __restrict__ logits, const float* __rest
     float best = -__builtin_inff();
     int bi = 0x7FFFFFFF;
     // ascending expert index, so strict > keeps the lowest index on ties
+    // (selects over non-short-circuit tests, as in argmax_step)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = l * 4 + i;
-      if (e < experts && (score[i] > best || bi == 0x7FFFFFFF)) {
-        best = score[i];
-        bi = e;
-      }
+      const bool take = (e < experts) & ((score[i] > best) | (bi == 0x7FFFFFFF));
+      best = take ? score[i] : best;
+      bi = take ? e : bi;
     }
     row_argmax(best, bi);
     chosen_id[rank] = bi;
     uint32_t bits = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (l * 4 + i == bi) {
-        bits = __float_as_uint(base[i]);
-        score[i] = -__builtin_inff();
-      }
+    for (int i = 0; i < 4; ++i) {
+      const bool mine_e = l * 4 + i == bi;
+      bits = mine_e ? __float_as_uint(base[i]) : bits;
+      score[i] = mine_e ? -__builtin_inff() : score[i];
+    }
     bits = or_step<0xB1>(bits);
     bits = or_step<0x4E>(bits);
     bits = or_step<0x141>(bits);
