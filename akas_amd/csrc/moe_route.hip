@@ -333,13 +333,22 @@ __global__ __launch_bounds__(1024) void routes_kernel(const int32_t* __restrict_
   int64_t base = 0;
   for (int64_t r0 = 0; r0 < rows; r0 += 1024) {
     const int64_t row = r0 + tid;
+    // Up to 32 ranks, the row's matches are kept as a bit mask, so its ids
+    // are read once (with its activity flag, in one round trip) for both
+    // the count and the writes.
     int cnt = 0;
-    if (row < rows && (!active || active[row] != 0)) {
+    uint32_t mask = 0;
+    if (row < rows) {
+      const bool act = !active || active[row] != 0;
       if (extra) {
         cnt = 1;
+      } else if (top <= 32) {
+        for (int k = 0; k < top; ++k) mask |= (uint32_t)(ids[row * top + k] == e) << k;
+        cnt = __builtin_popcount(mask);
       } else {
         for (int k = 0; k < top; ++k) cnt += ids[row * top + k] == e;
       }
+      if (!act) cnt = 0;
     }
     const int incl = wave_inclusive_scan(cnt, lane);
     if (lane == 63) wave_tot[wave] = incl;
@@ -355,6 +364,11 @@ __global__ __launch_bounds__(1024) void routes_kernel(const int32_t* __restrict_
       int64_t pos = base + before + incl - cnt;
       if (extra) {
         if (pos < rows) out[pos] = (int32_t)(row * ld + top);
+      } else if (top <= 32) {
+        for (uint32_t m = mask; m; m &= m - 1) {
+          if (pos < rows) out[pos] = (int32_t)(row * ld + __builtin_ctz(m));
+          ++pos;
+        }
       } else {
         for (int k = 0; k < top; ++k)
           if (ids[row * top + k] == e) {
