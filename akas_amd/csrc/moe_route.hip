@@ -663,6 +663,27 @@ __global__ __launch_bounds__(256) void combine8_kernel(const void* __restrict__ 
   const int64_t col = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
   if (col >= c) return;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  // SHARED: the gate and the shared row's eight values are requested before
+  // the ranks' loads, as one or two 16-byte loads where the row is 16-byte
+  // aligned (loaded element by element after the folds, each waited for the
+  // one before).  The row's alignment is the same for every lane, since col
+  // is a multiple of 8.
+  uint32_t graw = 0;  // the gate's bits, widened after the folds
+  u32x4 sraw[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+  bool svec = false;
+  const int64_t sbase = row * shared_ld + col;
+  if constexpr (SHARED) {
+    graw = gate_dtype == AKAS_DTYPE_F32 ? reinterpret_cast<const uint32_t*>(gate)[row]
+                                        : reinterpret_cast<const uint16_t*>(gate)[row];
+    const bool f32 = shared_dtype == AKAS_DTYPE_F32;
+    const uint8_t* at = reinterpret_cast<const uint8_t*>(shared) + sbase * (f32 ? 4 : 2);
+    svec = (reinterpret_cast<uintptr_t>(at) & 15) == 0;
+    if (svec) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(at);  // global, not flat, loads
+      sraw[0] = src[0];
+      if (f32) sraw[1] = src[1];
+    }
+  }
   // The contributions' loads are in bounds for every row, so they go out
   // without waiting for the row's flag, which only selects the result.
   {
@@ -711,11 +732,24 @@ __global__ __launch_bounds__(256) void combine8_kernel(const void* __restrict__ 
     for (int j = 0; j < 8; ++j) acc[j] = 0.f;
   }
   if constexpr (SHARED) {
-    const float g = round_bf16(load_elem(gate, row, gate_dtype));
+    const float gv = gate_dtype == AKAS_DTYPE_F32    ? __uint_as_float(graw)
+                     : gate_dtype == AKAS_DTYPE_BF16 ? bf16_bits_to_f32(graw)
+                                                      : f16_bits_to_f32(graw);
+    const float g = round_bf16(gv);
     const float den = 1.0f + expf(-g);
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      acc[j] += __fdiv_rn(round_bf16(load_elem(shared, row * shared_ld + col + j, shared_dtype)), den);
+    for (int j = 0; j < 8; ++j) {
+      float sv;
+      if (!svec)
+        sv = load_elem(shared, sbase + j, shared_dtype);
+      else if (shared_dtype == AKAS_DTYPE_F32)
+        sv = __uint_as_float(sraw[j >> 2][j & 3]);
+      else if (shared_dtype == AKAS_DTYPE_BF16)
+        sv = bf16_bits_to_f32((sraw[0][j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+      else
+        sv = f16_bits_to_f32((sraw[0][j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+      acc[j] += __fdiv_rn(round_bf16(sv), den);
+    }
   }
   float4* dst = reinterpret_cast<float4*>(out + row * c + col);
   dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
