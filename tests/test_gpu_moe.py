@@ -1168,6 +1168,35 @@ def test_moe_combine(dev, in_dtype, shared_dtype, rows, top, c):
     np.testing.assert_allclose(_np(out), exp, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("shared_dtype,gate_dtype", [("float32", "bfloat16"), ("bfloat16", "float32"),
+                                                      ("float16", "float16")])
+def test_moe_combine_shared_row_alignment(dev, shared_dtype, gate_dtype):
+    """The shared row is read as 16-byte loads where it is 16-byte aligned and
+    element by element where it is not (a contiguous view one element into
+    its storage): both give the oracle's result, bit for bit the same."""
+    import torch
+    from akas_amd import ops
+
+    rows, top, c = 37, 8, 512
+    rng = np.random.default_rng(61)
+    e = _t(rng.normal(0, 1, (rows, top, c)).astype(np.float32), dev, torch.bfloat16)
+    w = np.abs(rng.normal(0, 1, (rows, top))).astype(np.float32)
+    w /= w.sum(axis=1, keepdims=True)
+    sh = rng.normal(0, 1, (rows, c)).astype(np.float32)
+    g = _t(rng.normal(0, 2, rows).astype(np.float32), dev, getattr(torch, gate_dtype))
+    sdt = getattr(torch, shared_dtype)
+    aligned = _t(sh, dev, sdt)
+    store = torch.empty(rows * c + 1, dtype=sdt, device=dev)
+    store[1:] = aligned.reshape(-1)
+    unaligned = store[1:].view(rows, c)
+    assert unaligned.data_ptr() % 16 != 0 and unaligned.is_contiguous()
+    a = ops.moe_combine(e, _t(w, dev), aligned, g)
+    b = ops.moe_combine(e, _t(w, dev), unaligned, g)
+    exp = omoe.moe_combine(_np(e), w, _np(aligned), _np(g.float()))
+    np.testing.assert_array_equal(_np(a), _np(b))
+    np.testing.assert_allclose(_np(a), exp, rtol=1e-5, atol=1e-6)
+
+
 def _device_bank(dev, seed, shapes, std):
     """Block-quantized N(0, std) weights generated on the GPU: device codes
     and scales plus host copies for the oracle."""
