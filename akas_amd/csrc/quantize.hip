@@ -89,13 +89,21 @@ __global__ __launch_bounds__(256) void rms_quantize_kernel(const void* __restric
     const int64_t row = r0 + wave / WPR;
     const bool live = row < rows;
     const int64_t rbase = (live ? row : r0) * cols;
+    // All of the row's chunks are requested before the first is used (a
+    // load under its chunk's condition waited for the one before).
+    Raw8 raw[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int col = c0 + 512 * j + 8 * lane;
+      raw[j] = load8_raw<DT>(x, rbase + (col < c1 ? col : c0));
+    }
     float v[NJ][8];
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int col = c0 + 512 * j + 8 * lane;
       if (live && col < c1) {
-        load8<DT>(x, rbase + col, v[j]);
+        unpack8<DT>(raw[j], v[j]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[j][e], v[j][e], ss);
       } else {
