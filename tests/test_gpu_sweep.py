@@ -7,6 +7,10 @@ failure names a reproducible case:
   equation (src/akas/ops/linear/validation.py:206-230); the quantizer is
   checked bit for bit on the same input, and the prequantized binding and the
   K-partitioned product with its merge against the same reference;
+- the shared-expert block in one call: random token counts, widths, expert
+  counts up to 511, top-k and dtypes, bit for bit against its kinds composed
+  over a bank extended with the shared expert, and against the oracle's
+  block equation;
 - the routed MoE block: random token counts, hidden and expert widths,
   expert counts, top-k, routers (softmax or sigmoid + bias), packed or
   compact, fused or separate SwiGLU, intermediate policy, inactive rows and
@@ -125,4 +129,56 @@ def test_routed_moe_random_configurations(dev, case):
     assert np.isfinite(got).all(), label
     if use_active:
         assert np.all(got[active == 0] == 0), label
+    assert _rel_fro(got, exp) < 1e-2, label
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_shared_expert_block_random(dev, case):
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(3000 + case)
+    T = int(rng.choice([1, 2, 5, 16, 64, 100, 300, 700]))
+    H = int(128 * rng.choice([1, 2, 4, 8]))
+    F = int(128 * rng.choice([1, 2, 3, 4]))
+    E = int(rng.choice([2, 8, 32, 64, 128, 256, 511]))
+    while E * F * H > 32_000_000 and E > 2:
+        E //= 2
+    top = int(rng.integers(1, min(8, E) + 1))
+    xd, gd = str(rng.choice(_DT)), str(rng.choice(_DT))
+    sd = str(rng.choice(["float32", "bfloat16"]))
+    bank = {}
+    for name, shape in (("w1", (E, F, H)), ("w3", (E, F, H)), ("w2", (E, H, F)),
+                        ("sw1", (F, H)), ("sw3", (F, H)), ("sw2", (H, F))):
+        bank[name] = ofp8.quantize_weight_blocks(rng.normal(0, 0.05, shape).astype(np.float32), sd)
+    dbank = {n: (torch.from_numpy(c).to(dev), torch.from_numpy(s).to(dev).to(getattr(torch, sd)))
+             for n, (c, s) in bank.items()}
+    x = torch.from_numpy(bf16_normal(rng, (T, H))).to(dev).to(getattr(torch, xd))
+    logits = torch.from_numpy(rng.normal(0, 1, (T, E)).astype(np.float32)).to(dev)
+    gate = torch.from_numpy(rng.normal(0, 1.5, T).astype(np.float32)).to(dev).to(getattr(torch, gd))
+    args = [t for n in ("w1", "w3", "w2", "sw1", "sw3", "sw2") for t in dbank[n]]
+    out = ops.shared_expert_moe_block(x, logits, gate, *args, top=top)
+
+    ids, prob = ops.router(logits, top=top)
+    codes, scales = ops.quantize(x)
+    ext = torch.cat([ids, torch.full((T, 1), E, dtype=torch.int32, device=dev)], 1).contiguous()
+    counts, routes = ops.quantized_routes(ext, torch.ones(T, dtype=torch.int32, device=dev),
+                                          experts=E + 1)
+    full = {n: tuple(torch.cat([dbank[n][i], dbank["s" + n][i].unsqueeze(0)]).contiguous()
+                     for i in range(2)) for n in ("w1", "w3", "w2")}
+    act, act_scales = ops.fp8_expert_swiglu(codes, scales, *full["w1"], *full["w3"], counts, routes,
+                                            r=T, top=top + 1)
+    contrib = ops.expert_partial(act, act_scales, *full["w2"], counts, routes, r=T, top=top + 1,
+                                 routed_input=True, output_dtype=torch.bfloat16)
+    want = ops.moe_combine(contrib[:, :top].contiguous(), prob, contrib[:, top].contiguous(), gate)
+    torch.cuda.synchronize()
+    label = (T, H, F, E, top, xd, gd, sd)
+    got = out.cpu().numpy()
+    np.testing.assert_array_equal(got, want.cpu().numpy(), err_msg=str(label))
+    host = {n: (c, s.astype(np.float32)) for n, (c, s) in bank.items()}
+    exp = omoe.shared_expert_moe_layer(x.float().cpu().numpy(), logits.cpu().numpy(),
+                                       gate.float().cpu().numpy(),
+                                       *(a for n in ("w1", "w3", "w2", "sw1", "sw3", "sw2")
+                                         for a in host[n]), top)
+    assert np.isfinite(got).all(), label
     assert _rel_fro(got, exp) < 1e-2, label
