@@ -164,14 +164,17 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
                router="biased_softmax_router", scale=1.0, normalize=True, fused_swiglu=True,
                packed=False, max_block_m=64, product_dtype=torch.float32,
                activation_dtype=torch.float32, contribution_dtype=torch.float32,
-               partitions=1, partition_maximum_rows=None, fused_combine=False,
-               return_routing=False):
+               partitions=1, partition_maximum_rows=None, packed_minimum_rows=1,
+               fused_combine=False, return_routing=False):
     """One routed MoE feed-forward: ``x [T, H]`` (f32/f16/bf16) -> f32 ``[T, H]``.
 
     ``partitions`` > 1 applies the reference's K-partition policy to batches
     of at most ``partition_maximum_rows`` rows (all batches when None), as
     its one-row decode seed does (``partitions: 2, partition_maximum_rows:
-    1``, src/akas/ops/moe/definition.py:637-652).  ``fused_combine`` folds
+    1``, src/akas/ops/moe/definition.py:637-652).  ``packed`` packs batches
+    of at least ``packed_minimum_rows`` rows, as the packing rewrite does
+    (``_pack_experts``, definition.py:951-965; the same seed packs from 2048
+    rows, so its decode batches run unpacked).  ``fused_combine`` folds
     ``routed_combine`` into the down projection's epilogue
     (``expert_combine``, the same result bit for bit).  It is off by default:
     handing every workgroup's contributions to another XCD inside the launch
@@ -184,6 +187,10 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
     if packed and not fused_swiglu:
         raise ValueError("packing requires the fused SwiGLU pair kernel")
     rows = x.shape[0]
+    if type(packed_minimum_rows) is not int or packed_minimum_rows < 1:
+        raise ValueError("expert packing minimum rows must be positive")
+    if packed and rows < packed_minimum_rows:
+        packed = False
     if partition_maximum_rows is not None and rows > partition_maximum_rows:
         partitions = 1
     if packed:

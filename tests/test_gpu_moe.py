@@ -996,6 +996,13 @@ def test_routed_moe_layer_partitions_policy(dev, rows, parts):
     packed = moe.routed_moe(xt, lt, None, wts, top=top, partitions=parts, packed=True)
     np.testing.assert_array_equal(
         _np(packed), _np(moe.routed_moe(xt, lt, None, wts, top=top, packed=True)))
+    # The seed packs from packed_minimum_rows rows on (definition.py:951-965):
+    # a smaller batch runs the compact block, with its partitions.
+    seed = moe.routed_moe(xt, lt, None, wts, top=top, partitions=parts, packed=True,
+                          packed_minimum_rows=rows + 1)
+    np.testing.assert_array_equal(_np(seed), _np(out))
+    with pytest.raises(ValueError):
+        moe.routed_moe(xt, lt, None, wts, top=top, packed=True, packed_minimum_rows=0)
 
 
 @pytest.mark.parametrize("rows,packed,fused,policy", [
