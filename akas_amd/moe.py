@@ -89,7 +89,7 @@ class SharedExpert:
 
 def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed, max_block_m,
                           product_dtype, activation_dtype, contribution_dtype, quantized=None,
-                          partitions=1, combine_weights=None):
+                          partitions=1, combine_weights=None, separate_quantize=False):
     """Routes, FP8 activations and the grouped expert products:
     ``[T, top, H]`` contributions in ``contribution_dtype``.  ``quantized``:
     x's codes and scales when the caller made them already.  ``partitions``
@@ -127,7 +127,17 @@ def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed,
                                      tile_experts, tile_rows, routed_input=True,
                                      partitions=partitions, **common)
         return ops.expert_merge(partial, output_dtype=contribution_dtype), counts, routes, None
-    if fused_swiglu:
+    if fused_swiglu and separate_quantize:
+        # the paired kernel stores the activations unquantized and quantize
+        # follows (_separate_expert_quantize, src/akas/ops/moe/definition.py:
+        # 1056-1120): the same codes as the fused epilogue
+        activated = ops.expert_swiglu(
+            codes, scales, weights.w1, weights.s1, weights.w3, weights.s3, counts, routes,
+            tile_experts, tile_rows, offsets, product_dtype=product_dtype,
+            activation_dtype=activation_dtype, output_dtype=activation_dtype,
+            packed_input=packed, packed_output=packed, **common)
+        act, act_scales = ops.quantize(activated) if packed else ops.quantize(activated, top=top)
+    elif fused_swiglu:
         act_rows = ((ops.tile_capacity(rows, top, experts, max_block_m) * max_block_m,) if packed
                     else (rows, top))
         act, act_scales = ops.fp8_expert_swiglu(
@@ -165,6 +175,7 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
                packed=False, max_block_m=64, product_dtype=torch.float32,
                activation_dtype=torch.float32, contribution_dtype=torch.float32,
                partitions=1, partition_maximum_rows=None, packed_minimum_rows=1,
+               fused_quantize_minimum_rows=None, separate_activation_quantize=False,
                fused_combine=False, return_routing=False):
     """One routed MoE feed-forward: ``x [T, H]`` (f32/f16/bf16) -> f32 ``[T, H]``.
 
@@ -174,7 +185,12 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
     1``, src/akas/ops/moe/definition.py:637-652).  ``packed`` packs batches
     of at least ``packed_minimum_rows`` rows, as the packing rewrite does
     (``_pack_experts``, definition.py:951-965; the same seed packs from 2048
-    rows, so its decode batches run unpacked).  ``fused_combine`` folds
+    rows, so its decode batches run unpacked).  With ``fused_swiglu``, the
+    activations' FP8 quantization is fused into the gate/up launch for
+    batches of at least ``fused_quantize_minimum_rows`` rows; smaller
+    batches, or all with ``separate_activation_quantize``, store the
+    activations unquantized and run quantize after (definition.py:442-540,
+    :1056-1120, :1194-1200); the codes are the same.  ``fused_combine`` folds
     ``routed_combine`` into the down projection's epilogue
     (``expert_combine``, the same result bit for bit).  It is off by default:
     handing every workgroup's contributions to another XCD inside the launch
@@ -186,7 +202,14 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
         raise ValueError("unknown routed expert scoring")
     if packed and not fused_swiglu:
         raise ValueError("packing requires the fused SwiGLU pair kernel")
+    if fused_quantize_minimum_rows is not None:
+        if type(fused_quantize_minimum_rows) is not int or fused_quantize_minimum_rows < 1:
+            raise ValueError("expert quantization minimum rows must be a positive integer")
+        if not fused_swiglu:
+            raise ValueError("expert quantization minimum rows requires SwiGLU fusion")
     rows = x.shape[0]
+    separate_quantize = bool(separate_activation_quantize) or (
+        fused_quantize_minimum_rows is not None and rows < fused_quantize_minimum_rows)
     if type(packed_minimum_rows) is not int or packed_minimum_rows < 1:
         raise ValueError("expert packing minimum rows must be positive")
     if packed and rows < packed_minimum_rows:
@@ -218,7 +241,8 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
         max_block_m=max_block_m, product_dtype=product_dtype,
         activation_dtype=activation_dtype, contribution_dtype=contribution_dtype,
         quantized=quantized, partitions=partitions,
-        combine_weights=probability if fused_combine and partitions == 1 else None)
+        combine_weights=probability if fused_combine and partitions == 1 else None,
+        separate_quantize=separate_quantize)
     if out is None:
         out = ops.routed_combine(contributions, probability, active)
     if return_routing:

@@ -1005,6 +1005,42 @@ def test_routed_moe_layer_partitions_policy(dev, rows, parts):
         moe.routed_moe(xt, lt, None, wts, top=top, packed=True, packed_minimum_rows=0)
 
 
+@pytest.mark.parametrize("rows,packed,policy", [(8, False, "float32"), (200, False, "bfloat16"),
+                                                (300, True, "bfloat16")])
+def test_routed_moe_separate_activation_quantize(dev, rows, packed, policy):
+    """The separate-quantize rewrite (expert_swiglu stores the activations
+    unquantized, quantize follows; src/akas/ops/moe/definition.py:1056-1120),
+    and the fused quantize's minimum rows below which that form runs
+    (:1194-1200), give the fused block's result bit for bit."""
+    import torch
+    from akas_amd import moe
+
+    rng = np.random.default_rng(rows + 5)
+    H, F, E, top = 256, 384, 16, 4
+    x = bf16_normal(rng, (rows, H))
+    logits = rng.normal(0, 1, (rows, E)).astype(np.float32)
+    bank = {}
+    for name, shape in (("w1", (E, F, H)), ("w3", (E, F, H)), ("w2", (E, H, F))):
+        bank[name] = ofp8.quantize_weight_blocks(rng.normal(0, 0.05, shape).astype(np.float32))
+    wts = moe.ExpertWeights(*(_t(a, dev) for n in ("w1", "w3", "w2") for a in bank[n]))
+    xt, lt = _t(x, dev, torch.bfloat16), _t(logits, dev)
+    dt = getattr(torch, policy)
+    kw = dict(top=top, packed=packed, max_block_m=128 if packed else 64, product_dtype=dt,
+              activation_dtype=dt, contribution_dtype=dt)
+    fused = _np(moe.routed_moe(xt, lt, None, wts, **kw))
+    separate = _np(moe.routed_moe(xt, lt, None, wts, separate_activation_quantize=True, **kw))
+    below = _np(moe.routed_moe(xt, lt, None, wts, fused_quantize_minimum_rows=rows + 1, **kw))
+    above = _np(moe.routed_moe(xt, lt, None, wts, fused_quantize_minimum_rows=rows, **kw))
+    np.testing.assert_array_equal(separate, fused)
+    np.testing.assert_array_equal(below, fused)
+    np.testing.assert_array_equal(above, fused)
+    with pytest.raises(ValueError):
+        moe.routed_moe(xt, lt, None, wts, top=top, fused_quantize_minimum_rows=0)
+    with pytest.raises(ValueError):
+        moe.routed_moe(xt, lt, None, wts, top=top, fused_swiglu=False,
+                       fused_quantize_minimum_rows=4)
+
+
 @pytest.mark.parametrize("rows,packed,fused,policy", [
     (256, False, True, "bfloat16"), (256, False, False, "bfloat16"),
     (1000, True, True, "bfloat16"), (300, False, True, "float32")])
