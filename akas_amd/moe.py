@@ -176,7 +176,7 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
                activation_dtype=torch.float32, contribution_dtype=torch.float32,
                partitions=1, partition_maximum_rows=None, packed_minimum_rows=1,
                fused_quantize_minimum_rows=None, separate_activation_quantize=False,
-               fused_combine=False, return_routing=False):
+               block_m=None, fused_combine=False, return_routing=False):
     """One routed MoE feed-forward: ``x [T, H]`` (f32/f16/bf16) -> f32 ``[T, H]``.
 
     ``partitions`` > 1 applies the reference's K-partition policy to batches
@@ -190,7 +190,11 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
     batches of at least ``fused_quantize_minimum_rows`` rows; smaller
     batches, or all with ``separate_activation_quantize``, store the
     activations unquantized and run quantize after (definition.py:442-540,
-    :1056-1120, :1194-1200); the codes are the same.  ``fused_combine`` folds
+    :1056-1120, :1194-1200); the codes are the same.  ``block_m``, the
+    rewrite's row tile (16, 32, 64 or 128, at most ``max_block_m``;
+    definition.py:1499-1560), is checked as the reference checks it and
+    changes nothing else: the grouped kernels pick their row tiles on the
+    device, and no row tile changes a result.  ``fused_combine`` folds
     ``routed_combine`` into the down projection's epilogue
     (``expert_combine``, the same result bit for bit).  It is off by default:
     handing every workgroup's contributions to another XCD inside the launch
@@ -207,6 +211,11 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
             raise ValueError("expert quantization minimum rows must be a positive integer")
         if not fused_swiglu:
             raise ValueError("expert quantization minimum rows requires SwiGLU fusion")
+    if block_m is not None:
+        if type(block_m) is not int or block_m not in (16, 32, 64, 128):
+            raise ValueError("compact expert block_m must be 16, 32, 64 or 128")
+        if block_m > max_block_m:
+            raise ValueError("expert row tile exceeds its shared map's maximum")
     rows = x.shape[0]
     separate_quantize = bool(separate_activation_quantize) or (
         fused_quantize_minimum_rows is not None and rows < fused_quantize_minimum_rows)

@@ -1039,6 +1039,13 @@ def test_routed_moe_separate_activation_quantize(dev, rows, packed, policy):
     with pytest.raises(ValueError):
         moe.routed_moe(xt, lt, None, wts, top=top, fused_swiglu=False,
                        fused_quantize_minimum_rows=4)
+    # the rewrite's row tile: checked as the reference checks it, no effect
+    tiled = _np(moe.routed_moe(xt, lt, None, wts, block_m=32, **kw))
+    np.testing.assert_array_equal(tiled, fused)
+    with pytest.raises(ValueError):
+        moe.routed_moe(xt, lt, None, wts, top=top, block_m=48)
+    with pytest.raises(ValueError):
+        moe.routed_moe(xt, lt, None, wts, top=top, block_m=128, max_block_m=64)
 
 
 @pytest.mark.parametrize("rows,packed,fused,policy", [
