@@ -38,9 +38,13 @@ AKAS_DEV int lds_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row & 
 template <int BM, int BN, int THREADS>
 struct StagePlan {
   static constexpr int RSTEP = THREADS / 8;
-  static constexpr int CA = BM / RSTEP;
+  // A_PART: fewer A rows than thread rows (a 16-row tile on 256 threads):
+  // the threads of the first BM rows move one A chunk each, the others none.
+  static constexpr bool A_PART = BM < RSTEP;
+  static constexpr int CA = A_PART ? 1 : BM / RSTEP;
   static constexpr int CB = BN / RSTEP;
-  static_assert(BM % RSTEP == 0 && BN % RSTEP == 0, "tile rows must divide the thread rows");
+  static_assert((BM % RSTEP == 0 || (A_PART && RSTEP % BM == 0)) && BN % RSTEP == 0,
+                "tile rows must divide the thread rows");
   static_assert(THREADS >= 128, "swizzle invariance needs >= 16 thread rows");
   const uint8_t* a_base;  // uniform A base
   const uint8_t* b_base;  // uniform B base
@@ -48,6 +52,7 @@ struct StagePlan {
   uint32_t b_off;         // B byte offset of this thread's first row (k-block 0)
   uint32_t b_step;        // bytes between this thread's successive B rows
   int dst0;               // LDS offset of this thread's first chunk
+  bool a_live = true;     // this thread moves A chunks (always unless A_PART)
 
   // Staging registers are kept in two small arrays (A chunks, B chunks):
   // one 128-byte array of uint4 is past what the alloca promotion keeps in
@@ -55,7 +60,8 @@ struct StagePlan {
   AKAS_DEV void fetch(int kb, u32x4 (&ra)[CA], u32x4 (&rb)[CB]) const {
     const uint32_t ko = (uint32_t)kb * kBlock;
 #pragma unroll
-    for (int i = 0; i < CA; ++i) ra[i] = *reinterpret_cast<const u32x4*>(a_base + (a_off[i] + ko));
+    for (int i = 0; i < CA; ++i)
+      if (!A_PART || a_live) ra[i] = *reinterpret_cast<const u32x4*>(a_base + (a_off[i] + ko));
 #pragma unroll
     for (int j = 0; j < CB; ++j)
       rb[j] = *reinterpret_cast<const u32x4*>(b_base + (b_off + j * b_step + ko));
@@ -63,7 +69,7 @@ struct StagePlan {
   AKAS_DEV void stash(uint8_t* stage, const u32x4 (&ra)[CA], const u32x4 (&rb)[CB]) const {
 #pragma unroll
     for (int i = 0; i < CA; ++i)
-      *reinterpret_cast<u32x4*>(stage + dst0 + i * RSTEP * 128) = ra[i];
+      if (!A_PART || a_live) *reinterpret_cast<u32x4*>(stage + dst0 + i * RSTEP * 128) = ra[i];
 #pragma unroll
     for (int j = 0; j < CB; ++j)
       *reinterpret_cast<u32x4*>(stage + BM * 128 + dst0 + j * RSTEP * 128) = rb[j];

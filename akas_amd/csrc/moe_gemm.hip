@@ -297,7 +297,8 @@ AKAS_DEV void wave_priority_by_progress(int done, int total) {
 // SIMD, so that three workgroups share a CU.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int MODE, int OUT, int SDT, int STAGES = 0>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N)
-__attribute__((amdgpu_waves_per_eu((STAGES == 1 && BM == 32 && paired_mode(MODE)) ? 3 : 1)))
+__attribute__((amdgpu_waves_per_eu((STAGES == 1 && BM == 16 && paired_mode(MODE)) ? 4
+                                   : (STAGES == 1 && BM == 32 && paired_mode(MODE)) ? 3 : 1)))
 void expert_tiled_kernel(ExpertArgs p) {
   constexpr int THREADS = 64 * WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
@@ -355,7 +356,8 @@ void expert_tiled_kernel(ExpertArgs p) {
     const int row = tid >> 3, ch = tid & 7;
 #pragma unroll
     for (int i = 0; i < Plan::CA; ++i)
-      plan.a_off[i] = (uint32_t)rows_src[row + i * Plan::RSTEP] * (uint32_t)p.K + ch * 16;
+      plan.a_off[i] = (uint32_t)rows_src[min(row + i * Plan::RSTEP, BM - 1)] * (uint32_t)p.K + ch * 16;
+    plan.a_live = row < BM;
     plan.a_base = p.x;
     if constexpr (PAIRED) {
       // B row rho: 16-row tile j = rho/16 is gate (even j) or up (odd j)
@@ -867,7 +869,12 @@ static void launch_paired(const ExpertArgs& a, hipStream_t s) {
   // 135.5 us); when they do not, the two-stage tile's faster workgroups win
   // (Qwen3.5 block, about 900 workgroups: 184.0 against 191.4 us one-stage).
   const int64_t decode_tiles = std::min<int64_t>(a.E, (int64_t)a.r * a.top) * (a.N / 128) * a.parts;
-  if (mean <= 48 && decode_tiles <= 3 * (int64_t)device_cus()) {
+  if (mean <= 8 && decode_tiles <= 4 * (int64_t)device_cus() + device_cus() / 4) {
+    // a few rows per expert: 16-row tiles, four workgroups per CU
+    ExpertArgs b = a;
+    b.fair = decode_tiles >= 2 * (int64_t)device_cus();
+    launch_expert<16, 256, 1, 4, MODE, OUT, 1>(b, s);
+  } else if (mean <= 48 && decode_tiles <= 3 * (int64_t)device_cus()) {
     // one round: progress-ordered priority once workgroups share CUs
     ExpertArgs b = a;
     b.fair = decode_tiles >= 2 * (int64_t)device_cus();
