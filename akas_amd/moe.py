@@ -310,6 +310,8 @@ def shared_expert_moe(x, logits, shared_gate, weights: ExpertWeights, shared: Sh
     (64 tokens, 256 experts, top 8, H 2048, F 512: 180-181 us with the
     second stream; 168 us without any shared expert.)
     """
+    if routed_kinds not in ("routes", "groups"):
+        raise ValueError(f"unknown routed_kinds {routed_kinds!r}")
     rows = x.shape[0]
     if (shared_as_expert and routed_kinds == "routes" and fused_swiglu and not packed
             and ops._torch_dtype(contribution_dtype) in (torch.bfloat16, torch.float32)
@@ -336,13 +338,11 @@ def shared_expert_moe(x, logits, shared_gate, weights: ExpertWeights, shared: Sh
     ids, probability = ops.router(logits, top=top)
     if routed_kinds == "groups":
         contributions = _group_contributions(x, ids, weights, top=top)
-    elif routed_kinds == "routes":
+    else:
         contributions, _, _, _ = _expert_contributions(
             x, ids, _all_active(rows, x.device), weights, top=top, fused_swiglu=fused_swiglu,
             packed=packed, max_block_m=max_block_m, product_dtype=torch.float32,
             activation_dtype=torch.float32, contribution_dtype=contribution_dtype)
-    else:
-        raise ValueError(f"unknown routed_kinds {routed_kinds!r}")
     main.wait_stream(side)
     shared_out.record_stream(main)  # made on the side stream, read on this one
     return ops.moe_combine(contributions, probability, shared_out, shared_gate)
