@@ -50,6 +50,8 @@ SIGNATURES = {
                                  _i, _i, _i64, _i64, _i, _i, _i, _p]),
     "akas_fp8_expert_swiglu": (_i, [_p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _p,
                                     _i64, _i, _i, _i64, _i64, _i, _i, _i, _i, _i, _p]),
+    "akas_routed_fp8_expert_swiglu": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _p,
+                                           _i64, _i, _i, _i64, _i64, _i, _i, _p]),
     "akas_expert_swiglu": (_i, [_p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _i, _i64, _i,
                                 _i, _i64, _i64, _i, _i, _i, _i, _i, _p]),
     "akas_expert_pair_partial": (_i, [_p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _i64,

@@ -57,14 +57,21 @@ struct StagePlan {
   // Staging registers are kept in two small arrays (A chunks, B chunks):
   // one 128-byte array of uint4 is past what the alloca promotion keeps in
   // registers and would be placed in scratch.
-  AKAS_DEV void fetch(int kb, u32x4 (&ra)[CA], u32x4 (&rb)[CB]) const {
+  AKAS_DEV void fetch_a(int kb, u32x4 (&ra)[CA]) const {
     const uint32_t ko = (uint32_t)kb * kBlock;
 #pragma unroll
     for (int i = 0; i < CA; ++i)
       if (!A_PART || a_live) ra[i] = *reinterpret_cast<const u32x4*>(a_base + (a_off[i] + ko));
+  }
+  AKAS_DEV void fetch_b(int kb, u32x4 (&rb)[CB]) const {
+    const uint32_t ko = (uint32_t)kb * kBlock;
 #pragma unroll
     for (int j = 0; j < CB; ++j)
       rb[j] = *reinterpret_cast<const u32x4*>(b_base + (b_off + j * b_step + ko));
+  }
+  AKAS_DEV void fetch(int kb, u32x4 (&ra)[CA], u32x4 (&rb)[CB]) const {
+    fetch_a(kb, ra);
+    fetch_b(kb, rb);
   }
   AKAS_DEV void stash(uint8_t* stage, const u32x4 (&ra)[CA], const u32x4 (&rb)[CB]) const {
 #pragma unroll

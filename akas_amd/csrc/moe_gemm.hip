@@ -47,10 +47,13 @@ struct ExpertArgs {
   void* out;
   void* out2;          // up partials (expert_pair_partial)
   float* out_scales;
-  // expert_combine: the routed_combine fold in the epilogue
+  // expert_combine: the routed_combine fold in the epilogue; the fused
+  // route scan (SCAN kernels): the ids and active flags it scans
   const int32_t* ids;       // [r, top] expert ids (a rank is live when 0 <= id < E)
   const float* cweights;    // [r, top] combine weights
   const int32_t* active;    // [r] or null (every row active)
+  int32_t* scan_counts;     // SCAN: counts [E] written for the later launches
+  int32_t* scan_routes;     // SCAN: routes [E, r] written for the later launches
   float* cout;              // [r, N] f32 combined rows
   int32_t* arrivals;        // [r, N / BN] per (row, column block) arrival counts
   int r, top, E, N, K;
@@ -96,18 +99,21 @@ AKAS_DEV bool tile_in_chunk(int n, int c, int e0, int t, int r, int lane, int& b
 // registers: one memory round trip, where separate passes and the count read
 // again after them took three in series.  More experts read counts once per
 // pass, 64 at a time.
+// Up to 64 experts: c is lane e's count (0 past the experts).
+AKAS_DEV bool find_item_64(int c, int r, int bm, int tiles_n, int lane, Item& it) {
+  const int n = (c + bm - 1) / bm;
+  const int items = wave_sum_i(n) * tiles_n;
+  const int id = xcd_remap(blockIdx.x, items);
+  if (id >= items) return false;
+  it.nb = id % tiles_n;
+  int base = 0;
+  return tile_in_chunk(n, c, 0, id / tiles_n, r, lane, base, it);
+}
+
 AKAS_DEV bool find_item(const int32_t* counts, int experts, int r, int bm, int tiles_n, int lane,
                         Item& it) {
-  if (experts <= 64) {
-    const int c = lane < experts ? max(counts[lane], 0) : 0;
-    const int n = (c + bm - 1) / bm;
-    const int items = wave_sum_i(n) * tiles_n;
-    const int id = xcd_remap(blockIdx.x, items);
-    if (id >= items) return false;
-    it.nb = id % tiles_n;
-    int base = 0;
-    return tile_in_chunk(n, c, 0, id / tiles_n, r, lane, base, it);
-  }
+  if (experts <= 64)
+    return find_item_64(lane < experts ? max(counts[lane], 0) : 0, r, bm, tiles_n, lane, it);
   int total = 0;
   for (int e0 = 0; e0 < experts; e0 += 64) {
     const int e = e0 + lane;
@@ -162,6 +168,105 @@ AKAS_DEV void tile_row(const ExpertArgs& p, int e, int idx, bool live, int& src,
   src = row < 0 ? 0 : (row >= p.x_rows ? p.x_rows - 1 : row);
   const int d = live ? (p.packed_out ? off + idx : route) : -1;
   dst = d < p.out_rows ? d : -1;
+}
+
+// ---------------------------------------------------------------------------
+// The route scan fused into the decode gate/up launch (quantized_routes,
+// src/akas/ops/moe/kernel.py:121-151, done by every workgroup for itself).
+// Up to 64 experts and 4096 (row, rank) entries f = row * top + rank of ids
+// [r, top]: thread t of the 256 holds entries t + 256j, so each pass j reads
+// 1 KB of ids in one coalesced load per wave (every workgroup of the launch
+// reads the same lines; per-lane strided loads cost the launch 6 us).  An
+// expert's route at position q is its q-th live entry in f order; counts[e]
+// = min(entries, r), as the route tables hold at most r routes per expert.
+// ---------------------------------------------------------------------------
+constexpr int kScanThreads = 256;
+constexpr int kScanPasses = 16;
+constexpr int kScanMaxEntries = kScanThreads * kScanPasses;
+constexpr int kScanMaxExperts = 64;
+constexpr int kScanMaxTop = 64;
+
+// Row of entry f (f < 65536, top <= 64): the high word of f * ceil(2^32/top)
+// equals f / top over that whole range (checked exhaustively).
+AKAS_DEV int scan_row(int f, uint32_t magic) {
+  return magic ? (int)__umulhi((uint32_t)f, magic) : f;
+}
+
+// Entry t + 256j of this thread: its expert id, or -1 past the end, for an
+// inactive row or an id outside 0 .. E-1.  Every load is issued before the
+// first is used.
+AKAS_DEV void scan_entries(const ExpertArgs& p, int tid, uint32_t magic, int (&id)[kScanPasses]) {
+  const int n = p.r * p.top;
+  int raw[kScanPasses], act[kScanPasses];
+#pragma unroll
+  for (int j = 0; j < kScanPasses; ++j) {
+    const int f = tid + kScanThreads * j;
+    raw[j] = -1;
+    act[j] = 1;
+    if (f < n) {
+      raw[j] = p.ids[f];
+      if (p.active) act[j] = p.active[scan_row(f, magic)];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kScanPasses; ++j)
+    id[j] = ((act[j] != 0) & ((unsigned)raw[j] < (unsigned)p.E)) ? raw[j] : -1;
+}
+
+// counts [E] (workgroup 0) and the -1 padding of routes [E, r] past each
+// expert's count (expert e by workgroup e, e + grid, ...): the tables
+// quantized_routes leaves, for the launches after this one.
+AKAS_DEV void scan_tables(const ExpertArgs& p, const int* hist, int tid) {
+  if (blockIdx.x == 0 && tid < p.E) p.scan_counts[tid] = min(hist[tid], p.r);
+  for (int e = blockIdx.x; e < p.E; e += gridDim.x) {
+    int32_t* out = p.scan_routes + (int64_t)e * p.r;
+    for (int i = min(hist[e], p.r) + tid; i < p.r; i += kScanThreads) out[i] = -1;
+  }
+}
+
+// Rows row0 .. row0+BM-1 of expert e's routes (count of them live): source
+// rows and scatter destinations into rows_src / rows_dst (rows past count
+// repeat the first row's source and scatter nowhere), and, from column
+// block 0's workgroup, the routes themselves into scan_routes.  A pass's
+// matches are numbered by wave ballots and per-wave totals in LDS.
+template <int BM>
+AKAS_DEV void scan_tile_rows(const ExpertArgs& p, const int (&id)[kScanPasses], uint32_t magic,
+                             int e, int row0, int count, bool write_routes, int tid,
+                             int (*wave_count)[4], int* rows_src, int* rows_dst) {
+  const int lane = tid & 63, wave = tid >> 6;
+  const uint64_t below = (uint64_t{1} << lane) - 1;
+  uint64_t hit[kScanPasses];
+#pragma unroll
+  for (int j = 0; j < kScanPasses; ++j) hit[j] = __ballot(id[j] == e);
+  if (lane < kScanPasses) {
+    uint64_t h = hit[0];
+#pragma unroll
+    for (int j = 1; j < kScanPasses; ++j) h = lane == j ? hit[j] : h;
+    wave_count[lane][wave] = __builtin_popcountll(h);
+  }
+  __syncthreads();
+  int32_t* routes = p.scan_routes + (int64_t)e * p.r;
+  int done = 0;  // matches in the passes before j
+#pragma unroll
+  for (int j = 0; j < kScanPasses; ++j) {
+    const int c0 = wave_count[j][0], c1 = wave_count[j][1], c2 = wave_count[j][2],
+              c3 = wave_count[j][3];
+    const int before = (wave > 0 ? c0 : 0) + (wave > 1 ? c1 : 0) + (wave > 2 ? c2 : 0);
+    const int pos = done + before + __builtin_popcountll(hit[j] & below);
+    if ((id[j] == e) & (pos >= row0) & (pos < row0 + BM) & (pos < count)) {
+      const int f = tid + kScanThreads * j;
+      const int src = scan_row(f, magic);
+      rows_src[pos - row0] = src;
+      rows_dst[pos - row0] = f;
+      if (write_routes) routes[pos] = f;
+      if (pos == row0)
+        for (int i = count - row0; i < BM; ++i) {
+          rows_src[i] = src;
+          rows_dst[i] = -1;
+        }
+    }
+    done += c0 + c1 + c2 + c3;
+  }
 }
 
 // Epilogue modes of the grouped kernels.  Modes 1-3 share the paired tile:
@@ -295,7 +400,10 @@ AKAS_DEV void wave_priority_by_progress(int done, int total) {
 // STAGES: LDS stages (0: one for the 32-row expert partial, two otherwise).
 // The one-stage paired 32-row tile keeps its registers within three waves per
 // SIMD, so that three workgroups share a CU.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int MODE, int OUT, int SDT, int STAGES = 0>
+// SCAN: the workgroup scans ids itself (scan_entries) instead of reading the
+// route tables, and writes them for the launches after it.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int MODE, int OUT, int SDT, int STAGES = 0,
+          int SCAN = 0>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N)
 __attribute__((amdgpu_waves_per_eu((STAGES == 1 && BM == 16 && paired_mode(MODE)) ? 4
                                    : (STAGES == 1 && BM == 32 && paired_mode(MODE)) ? 3 : 1)))
@@ -322,9 +430,24 @@ void expert_tiled_kernel(ExpertArgs p) {
   __shared__ float row_max[MODE == kSwigluFp8 ? WAVES_N : 1][MODE == kSwigluFp8 ? BM : 1];
   __shared__ int taken[MODE == kCombine ? BM : 1];
   __shared__ int ntaken;
+  static_assert(!SCAN || THREADS == kScanThreads, "the route scan runs on 256 threads");
+  __shared__ int scan_hist[SCAN ? kScanMaxExperts : 1];
+  __shared__ int scan_wave[SCAN ? kScanPasses : 1][4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if constexpr (MODE == kCombine) zero_unrouted_rows<THREADS>(p);
+  int sid[SCAN ? kScanPasses : 1];
+  const uint32_t magic = p.top > 1 ? 0xFFFFFFFFu / (uint32_t)p.top + 1u : 0u;
+  if constexpr (SCAN) {
+    scan_entries(p, tid, magic, sid);
+    if (tid < kScanMaxExperts) scan_hist[tid] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kScanPasses; ++j)
+      if (sid[j] >= 0) atomicAdd(&scan_hist[sid[j]], 1);
+    __syncthreads();
+    scan_tables(p, scan_hist, tid);
+  }
   // Live items first, then the XCD remap (as in the prefill kernel): the
   // workgroups of the capacity-sized grid that find no tile come last and
   // exit, so the live ones spread evenly over the CUs.  Column block fastest:
@@ -332,7 +455,12 @@ void expert_tiled_kernel(ExpertArgs p) {
   // share its activation rows (LFM2 decode layer 145.5 -> 142.6 us, Qwen3.5
   // block 190.5 -> 183.2 us against tiles fastest over the whole grid).
   Item item;
-  if (!find_item(p.counts, p.E, p.r, BM, p.tiles_n, lane, item)) return;  // uniform
+  if constexpr (SCAN) {
+    const int c = lane < p.E ? min(scan_hist[lane], p.r) : 0;
+    if (!find_item_64(c, p.r, BM, p.tiles_n, lane, item)) return;  // uniform
+  } else if (!find_item(p.counts, p.E, p.r, BM, p.tiles_n, lane, item)) {
+    return;  // uniform
+  }
   const int nb = item.nb, e = item.expert, tile = item.tile, count = item.count;
   const int row0 = tile * BM;
   if (row0 >= count) return;  // only reachable with counts[e] > r
@@ -343,22 +471,11 @@ void expert_tiled_kernel(ExpertArgs p) {
 
   const ExpertSlice xs = expert_slice(p, e);
 
-  // Gathered source rows and scatter destinations of this tile.
-  for (int i = tid; i < BM; i += THREADS) {
-    const int idx = row0 + i;
-    const bool live = idx < count;
-    tile_row(p, e, live ? idx : row0, live, rows_src[i], rows_dst[i]);
-  }
-  __syncthreads();
-
   Plan plan;
+  u32x4 ra[Plan::CA], rb[Plan::CB];
+  const int prow = tid >> 3, pch = tid & 7;
   {
-    const int row = tid >> 3, ch = tid & 7;
-#pragma unroll
-    for (int i = 0; i < Plan::CA; ++i)
-      plan.a_off[i] = (uint32_t)rows_src[min(row + i * Plan::RSTEP, BM - 1)] * (uint32_t)p.K + ch * 16;
-    plan.a_live = row < BM;
-    plan.a_base = p.x;
+    const int row = prow, ch = pch;
     if constexpr (PAIRED) {
       // B row rho: 16-row tile j = rho/16 is gate (even j) or up (odd j)
       // column n0 + (rho/32)*16 + rho%16; the parity is fixed per thread.
@@ -373,6 +490,28 @@ void expert_tiled_kernel(ExpertArgs p) {
     }
     plan.dst0 = lds_off(row, ch);
   }
+  // With the route scan, the first weight k-block is requested before the
+  // scan's barriers, which then run under its latency.
+  if constexpr (SCAN) plan.fetch_b(kb0, rb);
+
+  // Gathered source rows and scatter destinations of this tile.
+  if constexpr (SCAN) {
+    scan_tile_rows<BM>(p, sid, magic, e, row0, count, nb == 0, tid, scan_wave, rows_src,
+                       rows_dst);
+  } else {
+    for (int i = tid; i < BM; i += THREADS) {
+      const int idx = row0 + i;
+      const bool live = idx < count;
+      tile_row(p, e, live ? idx : row0, live, rows_src[i], rows_dst[i]);
+    }
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int i = 0; i < Plan::CA; ++i)
+    plan.a_off[i] = (uint32_t)rows_src[min(prow + i * Plan::RSTEP, BM - 1)] * (uint32_t)p.K + pch * 16;
+  plan.a_live = prow < BM;
+  plan.a_base = p.x;
   const float* as_row = p.as + (int64_t)rows_src[tid < BM ? tid : 0] * KB;
 
   const int wm = wave % WAVES_M, wn = wave / WAVES_M;
@@ -386,11 +525,13 @@ void expert_tiled_kernel(ExpertArgs p) {
   // Every global load (data and both scales) is issued one k-block before its
   // use: loads complete in issue order, so a scale fetched after the
   // prefetch would make the current multiply wait for that prefetch.
-  u32x4 ra[Plan::CA], rb[Plan::CB];
   float ras, rws0, rws1 = 0.f;
   if constexpr (NSTAGE == 1) {
     // one stage: stash, prefetch the next k-block, barrier, multiply, barrier
-    plan.fetch(kb0, ra, rb);
+    if constexpr (SCAN)
+      plan.fetch_a(kb0, ra);
+    else
+      plan.fetch(kb0, ra, rb);
     ras = as_row[kb0];
     rws0 = load_scale_t<SDT>(xs.ws, ws_base + kb0);
     if constexpr (PAIRED) rws1 = load_scale_t<SDT>(xs.ws2, ws_base + kb0);
@@ -411,7 +552,10 @@ void expert_tiled_kernel(ExpertArgs p) {
     }
     __syncthreads();
   } else {
-    plan.fetch(kb0, ra, rb);
+    if constexpr (SCAN)
+      plan.fetch_a(kb0, ra);
+    else
+      plan.fetch(kb0, ra, rb);
     ras = as_row[kb0];
     float ws0 = load_scale_t<SDT>(xs.ws, ws_base + kb0);
     float ws1 = PAIRED ? load_scale_t<SDT>(xs.ws2, ws_base + kb0) : 0.f;
@@ -812,15 +956,17 @@ int64_t capacity_tiles(int64_t r, int64_t top, int64_t experts, int64_t bm) {
   return routes < b ? routes : b;
 }
 
-template <int BM, int BN, int WMW, int WNW, int MODE, int OUT, int STAGES = 0>
+template <int BM, int BN, int WMW, int WNW, int MODE, int OUT, int STAGES = 0, int SCAN = 0>
 static void launch_expert(ExpertArgs a, hipStream_t s) {
   a.max_tiles = (int)capacity_tiles(a.r, a.top, a.E, BM);
   a.tiles_n = paired_mode(MODE) ? a.N / (BN / 2) : a.N / BN;
   dim3 grid((unsigned)(a.max_tiles * a.tiles_n), (unsigned)a.parts);
   if (a.ws_dtype == AKAS_DTYPE_F32)
-    expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_F32, STAGES><<<grid, 64 * WMW * WNW, 0, s>>>(a);
+    expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_F32, STAGES, SCAN>
+        <<<grid, 64 * WMW * WNW, 0, s>>>(a);
   else
-    expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_BF16, STAGES><<<grid, 64 * WMW * WNW, 0, s>>>(a);
+    expert_tiled_kernel<BM, BN, WMW, WNW, MODE, OUT, AKAS_DTYPE_BF16, STAGES, SCAN>
+        <<<grid, 64 * WMW * WNW, 0, s>>>(a);
 }
 
 template <int MODE, int OUT>
@@ -857,8 +1003,9 @@ static void launch_partial(const ExpertArgs& a, hipStream_t s) {
 }
 
 // The paired kernels (modes 1-3), row tile by the mean rows per expert as
-// for expert_partial.
-template <int MODE, int OUT>
+// for expert_partial.  SCAN (the fused route scan) only where scan_fits
+// holds, which keeps it to the tiled kernels below 49 mean rows.
+template <int MODE, int OUT, int SCAN = 0>
 static void launch_paired(const ExpertArgs& a, hipStream_t s) {
   const int64_t mean = (int64_t)a.r * a.top / a.E;
   const bool aligned = MODE != kPairPartial || reinterpret_cast<uintptr_t>(a.out2) % 16 == 0;
@@ -873,22 +1020,33 @@ static void launch_paired(const ExpertArgs& a, hipStream_t s) {
     // a few rows per expert: 16-row tiles, four workgroups per CU
     ExpertArgs b = a;
     b.fair = decode_tiles >= 2 * (int64_t)device_cus();
-    launch_expert<16, 256, 1, 4, MODE, OUT, 1>(b, s);
+    launch_expert<16, 256, 1, 4, MODE, OUT, 1, SCAN>(b, s);
   } else if (mean <= 48 && decode_tiles <= 3 * (int64_t)device_cus()) {
     // one round: progress-ordered priority once workgroups share CUs
     ExpertArgs b = a;
     b.fair = decode_tiles >= 2 * (int64_t)device_cus();
-    launch_expert<32, 256, 1, 4, MODE, OUT, 1>(b, s);
-  } else if (mean <= 48)
-    launch_expert<32, 256, 1, 4, MODE, OUT>(a, s);
-  else if (aligned && expert_dma_fits(a, mean, dma::BN / 2))
-    launch_expert_dma<MODE, OUT>(a, s);
-  else
-    launch_expert<128, 256, 2, 4, MODE, OUT>(a, s);
+    launch_expert<32, 256, 1, 4, MODE, OUT, 1, SCAN>(b, s);
+  } else if (mean <= 48) {
+    launch_expert<32, 256, 1, 4, MODE, OUT, 0, SCAN>(a, s);
+  } else if constexpr (!SCAN) {
+    if (aligned && expert_dma_fits(a, mean, dma::BN / 2))
+      launch_expert_dma<MODE, OUT>(a, s);
+    else
+      launch_expert<128, 256, 2, 4, MODE, OUT>(a, s);
+  }
 }
 
 static void launch_swiglu(const ExpertArgs& a, hipStream_t s) {
   launch_paired<kSwigluFp8, AKAS_DTYPE_F32>(a, s);
+}
+
+// Shapes the fused route scan covers: a decode batch's routes (at least one
+// row, up to 4096 entries, at most 48 per expert on average, top <= 64) over
+// up to 64 experts.
+static bool scan_fits(int64_t r, int top, int experts) {
+  const int64_t n = r * top;
+  return r >= 1 && top <= kScanMaxTop && experts <= kScanMaxExperts && n <= kScanMaxEntries &&
+         n / experts <= 48;
 }
 
 static inline bool float_dtype(int d) {
@@ -1030,6 +1188,40 @@ extern "C" int akas_fp8_expert_swiglu(const uint8_t* x, const float* activation_
   a.parts = 1; a.kb_per_part = (int)(k / kBlock);
   a.ws_dtype = scale_dtype; a.prod_dtype = product_dtype; a.act_dtype = activation_dtype;
   launch_swiglu(a, reinterpret_cast<hipStream_t>(stream));
+  AKAS_CHECK_LAUNCH();
+  return AKAS_OK;
+}
+
+extern "C" int akas_routed_fp8_expert_swiglu(
+    const int32_t* ids, const int32_t* active, int32_t* counts, int32_t* routes, const uint8_t* x,
+    const float* activation_scales, const uint8_t* w, const void* w_scales, const uint8_t* w2,
+    const void* w2_scales, int scale_dtype, uint8_t* out, float* output_scales, int64_t r,
+    int top, int experts, int64_t o, int64_t k, int product_dtype, int activation_dtype,
+    void* stream) {
+  int st = check_common(r, top, experts, o, k, 32, 0, r);
+  if (st != AKAS_OK) return st;
+  if (!float_dtype(product_dtype) || !float_dtype(activation_dtype) || !scale_dtype_ok(scale_dtype))
+    return AKAS_ERR_DTYPE;
+  if (!counts) return AKAS_ERR_NULL;
+  if (r > 0 && (!ids || !routes || !x || !activation_scales || !w || !w_scales || !w2 ||
+                !w2_scales || !out || !output_scales))
+    return AKAS_ERR_NULL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ExpertArgs a{};
+  a.x = x; a.as = activation_scales; a.w = w; a.ws = w_scales; a.w2 = w2; a.ws2 = w2_scales;
+  a.counts = counts; a.routes = routes;
+  a.ids = ids; a.active = active; a.scan_counts = counts; a.scan_routes = routes;
+  a.out = out; a.out_scales = output_scales;
+  a.r = (int)r; a.top = top; a.E = experts; a.N = (int)o; a.K = (int)k;
+  a.x_rows = (int)r; a.out_rows = (int)(r * top);
+  a.parts = 1; a.kb_per_part = (int)(k / kBlock);
+  a.ws_dtype = scale_dtype; a.prod_dtype = product_dtype; a.act_dtype = activation_dtype;
+  if (scan_fits(r, top, experts)) {
+    launch_paired<kSwigluFp8, AKAS_DTYPE_F32, 1>(a, s);
+  } else {
+    launch_quantized_routes(ids, active, counts, routes, r, experts, top, s);
+    if (r > 0) launch_swiglu(a, s);
+  }
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }

@@ -1,5 +1,5 @@
 // Launches shared between the MoE sources: the routing side (moe_route.hip)
-// run by the shared-expert block entry point (moe_gemm.hip).
+// run by the entry points of the grouped expert kernels (moe_gemm.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -11,6 +11,11 @@ namespace akas {
 // weights [r, top].  Returns an AKAS status.
 int launch_decode_router(const float* logits, int32_t* ids, float* weights, int64_t r,
                          int experts, int top, hipStream_t s);
+
+// quantized_routes: counts [experts] and routes [experts, r] from ids
+// [r, top] and active [r] (null: every row active).
+void launch_quantized_routes(const int32_t* ids, const int32_t* active, int32_t* counts,
+                             int32_t* routes, int64_t r, int experts, int top, hipStream_t s);
 
 // quantized_routes over ids [r, top] for experts + 1 experts, every row
 // active: a route names the entry row * (top + 1) + rank, and expert

@@ -816,6 +816,18 @@ int launch_decode_router(const float* logits, int32_t* ids, float* weights, int6
   return AKAS_OK;
 }
 
+void launch_quantized_routes(const int32_t* ids, const int32_t* active, int32_t* counts,
+                             int32_t* routes, int64_t r, int experts, int top, hipStream_t s) {
+  // routes4_kernel's first pass loads ids[0..15] and active[0..3]
+  // unconditionally, so it needs at least four rows and the flags; an empty
+  // batch takes the generic kernel, which only writes counts[e] = 0.
+  if (top == 4 && r >= 4 && r % 4 == 0 && active &&
+      reinterpret_cast<uintptr_t>(active) % 16 == 0 && reinterpret_cast<uintptr_t>(ids) % 16 == 0)
+    routes4_kernel<<<experts, 1024, 0, s>>>(ids, active, counts, routes, r);
+  else
+    routes_kernel<<<experts, 1024, 0, s>>>(ids, active, counts, routes, r, top);
+}
+
 void launch_routes_with_shared(const int32_t* ids, int32_t* counts, int32_t* routes, int64_t r,
                                int experts, int top, hipStream_t s) {
   routes_kernel<<<experts + 1, 1024, 0, s>>>(ids, nullptr, counts, routes, r, top, top + 1);
@@ -912,15 +924,8 @@ extern "C" int akas_quantized_routes(const int32_t* ids, const int32_t* active, 
                                      void* stream) {
   if (r < 0 || experts < 1 || top < 1 || r * top > 0x7FFFFFFF) return AKAS_ERR_GEOMETRY;
   if (!counts || (r > 0 && (!ids || !active || !routes))) return AKAS_ERR_NULL;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // routes4_kernel's first pass loads ids[0..15] and active[0..3]
-  // unconditionally, so it needs at least four rows; an empty batch takes
-  // the generic kernel, which only writes counts[e] = 0.
-  if (top == 4 && r >= 4 && r % 4 == 0 && reinterpret_cast<uintptr_t>(active) % 16 == 0 &&
-      reinterpret_cast<uintptr_t>(ids) % 16 == 0)
-    routes4_kernel<<<experts, 1024, 0, s>>>(ids, active, counts, routes, r);
-  else
-    routes_kernel<<<experts, 1024, 0, s>>>(ids, active, counts, routes, r, top);
+  launch_quantized_routes(ids, active, counts, routes, r, experts, top,
+                          reinterpret_cast<hipStream_t>(stream));
   AKAS_CHECK_LAUNCH();
   return AKAS_OK;
 }

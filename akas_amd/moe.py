@@ -104,9 +104,17 @@ def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed,
     ``combined`` is its f32 ``[T, H]``; otherwise ``combined`` is None."""
     rows, hidden = x.shape
     experts = weights.experts
-    counts, routes = ops.quantized_routes(ids, active, experts=experts)
-    tile_experts = tile_rows = None  # the kernels locate tiles from counts
     codes, scales = ops.quantize(x) if quantized is None else quantized
+    # Unpacked fused SwiGLU: the route scan rides in the gate/up launch
+    # (one launch fewer per decode layer, the same tables and codes).
+    routed_gate_up = fused_swiglu and not packed and not separate_quantize and partitions == 1
+    if routed_gate_up:
+        counts, routes, act, act_scales = ops.routed_fp8_expert_swiglu(
+            ids, active, codes, scales, weights.w1, weights.s1, weights.w3, weights.s3,
+            product_dtype=product_dtype, activation_dtype=activation_dtype)
+    else:
+        counts, routes = ops.quantized_routes(ids, active, experts=experts)
+    tile_experts = tile_rows = None  # the kernels locate tiles from counts
     common = dict(r=rows, top=top, max_block_m=max_block_m)
     offsets = None
     if packed:
@@ -127,7 +135,9 @@ def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed,
                                      tile_experts, tile_rows, routed_input=True,
                                      partitions=partitions, **common)
         return ops.expert_merge(partial, output_dtype=contribution_dtype), counts, routes, None
-    if fused_swiglu and separate_quantize:
+    if routed_gate_up:
+        pass
+    elif fused_swiglu and separate_quantize:
         # the paired kernel stores the activations unquantized and quantize
         # follows (_separate_expert_quantize, src/akas/ops/moe/definition.py:
         # 1056-1120): the same codes as the fused epilogue

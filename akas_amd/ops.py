@@ -737,6 +737,41 @@ def fp8_expert_swiglu(x, activation_scales, w, scales, w2, scales2, counts, rout
     return out, output_scales
 
 
+@_on_tensor_device
+def routed_fp8_expert_swiglu(ids, active, x, activation_scales, w, scales, w2, scales2, *,
+                             product_dtype=torch.float32, activation_dtype=torch.float32,
+                             counts=None, routes=None, out=None, output_scales=None):
+    """``quantized_routes`` then ``fp8_expert_swiglu`` (unpacked rows) as one
+    call: ``(counts, routes, out, output_scales)``, each bit-identical to the
+    two kinds run in turn (src/akas/ops/moe/kernel.py:121-151,
+    src/akas/ops/moe/cuda.py:823-946).  ``active`` may be None (every row
+    active).  Decode batches (up to 64 experts, 4096 routes, 48 per expert on
+    average) take one launch, in which every workgroup scans ``ids`` itself.
+    """
+    _need(ids, "ids", torch.int32)
+    r, top = ids.shape
+    if active is not None:
+        _need(active, "active", torch.int32, (r,))
+    _need(w, "w", torch.uint8)
+    _need(w2, "w2", torch.uint8, tuple(w.shape))
+    experts, o, k = w.shape
+    sshape = (experts, (o + BLOCK - 1) // BLOCK, k // BLOCK)
+    _need(scales, "scales", _SCALES, sshape)
+    _need(scales2, "scales2", scales.dtype, sshape)
+    _need(x, "x", torch.uint8, (r, k))
+    _need(activation_scales, "activation_scales", torch.float32, (r, k // BLOCK))
+    counts = _out(counts, "counts", (experts,), torch.int32, ids)
+    routes = _out(routes, "routes", (experts, r), torch.int32, ids)
+    out = _out(out, "out", (r, top, o), torch.uint8, x)
+    output_scales = _out(output_scales, "output_scales", (r, top, o // BLOCK), torch.float32, x)
+    check(_lib.load().akas_routed_fp8_expert_swiglu(
+        _ptr(ids), _ptr(active), _ptr(counts), _ptr(routes), _ptr(x), _ptr(activation_scales),
+        _ptr(w), _ptr(scales), _ptr(w2), _ptr(scales2), _dt(scales.dtype), _ptr(out),
+        _ptr(output_scales), r, top, experts, o, k, _dt(product_dtype), _dt(activation_dtype),
+        _stream()), "routed_fp8_expert_swiglu")
+    return counts, routes, out, output_scales
+
+
 def _paired_inputs(x, activation_scales, w, scales, w2, scales2, counts, routes, r):
     _need(x, "x", torch.uint8)
     _need(w, "w", torch.uint8)

@@ -382,6 +382,28 @@ int akas_fp8_expert_swiglu(const uint8_t* x, const float* activation_scales, con
                            int packed_input, int packed_output, void* stream);
 
 /*
+ * quantized_routes followed by fp8_expert_swiglu (unpacked rows) in one
+ * launch: ids, active, x, activation_scales, w, scales, w2, scales2 ->
+ * counts, routes, out, output_scales.  No counterpart in the reference, which
+ * runs the two kinds one after the other (src/akas/ops/moe/kernel.py:121-151,
+ * src/akas/ops/moe/cuda.py:823-946); for callers that run both on a decode
+ * batch.  counts [experts] and routes [experts, r] are bit-identical to
+ * akas_quantized_routes' (the down projection and the combine read them),
+ * out u8 [r, top, o] and output_scales f32 [r, top, o/128] to
+ * akas_fp8_expert_swiglu's over those tables.  active [r] may be null
+ * (every row active).  One launch when experts <= 64, 1 <= r*top <= 4096 and
+ * r*top / experts <= 48 (every workgroup scans ids itself); otherwise the two
+ * kinds' launches.
+ */
+int akas_routed_fp8_expert_swiglu(const int32_t* ids, const int32_t* active, int32_t* counts,
+                                  int32_t* routes, const uint8_t* x,
+                                  const float* activation_scales, const uint8_t* w,
+                                  const void* w_scales, const uint8_t* w2, const void* w2_scales,
+                                  int scale_dtype, uint8_t* out, float* output_scales, int64_t r,
+                                  int top, int experts, int64_t o, int64_t k, int product_dtype,
+                                  int activation_dtype, void* stream);
+
+/*
  * expert_swiglu(r, top, experts, o, k[, product_dtype, activation_dtype,
  * output_dtype, max_block_m, packed_input, packed_output]), the FP8 paired
  * form: x, activation_scales, w, scales, w2, scales2, counts, routes,

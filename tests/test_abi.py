@@ -87,6 +87,15 @@ def test_host_validation_rejects_before_launch():
     # fused swiglu: packed output without packed input
     assert lib.akas_fp8_expert_swiglu(1, 1, 1, 1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 4, 2, 4, 128,
                                       256, 0, 0, 64, 0, 1, None) == -1
+    # routes + fused swiglu: o not a multiple of 128, product dtype code,
+    # scale dtype code, null x, null counts
+    rsw = lambda x, counts, sdt, o, pd: lib.akas_routed_fp8_expert_swiglu(
+        1, None, counts, 1, x, 1, 1, 1, 1, 1, sdt, 1, 1, 4, 2, 8, o, 256, pd, 0, None)
+    assert rsw(1, 1, 0, 100, 0) == -1
+    assert rsw(1, 1, 0, 128, 7) == -3
+    assert rsw(1, 1, 1, 128, 0) == -3
+    assert rsw(None, 1, 0, 128, 0) == -2
+    assert rsw(1, None, 0, 128, 0) == -2
     # shared-expert block: 1024 experts leave no index for the shared one, h
     # not a multiple of 128, gate dtype code, nulls, workspace, no rows
     blk = lambda x, gdt, ws, wsb, r, e, top, h, f: lib.akas_shared_expert_moe(

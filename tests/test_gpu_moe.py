@@ -482,6 +482,126 @@ def test_fused_swiglu_matches_separate_chain_bitwise(dev, rows, top, experts, o,
     assert rel_fro(got, exp) < 1e-2
 
 
+def _distinct_ids(rng, rows, top, experts):
+    """Each row's top ids: distinct experts in random order."""
+    return np.argsort(rng.random((rows, experts)), axis=1)[:, :top].astype(np.int32)
+
+
+# (rows, top, experts, o, k, active, scale dtype): one launch (16-row tiles at
+# up to 8 routes per expert, the one-round and the two-stage 32-row tiles,
+# rows past a 16-entry boundary, inactive rows, ids outside the bank, one
+# expert taking every row) and the two-launch shapes (4096 routes at 64 per
+# expert, 128 experts)
+ROUTED_SWIGLU_CASES = [(256, 4, 64, 256, 512, "ones", "float32"),
+                       (8, 4, 64, 256, 256, "ones", "bfloat16"),
+                       (3, 2, 8, 128, 256, None, "float32"),
+                       (100, 3, 32, 256, 384, "random", "bfloat16"),
+                       (37, 3, 16, 128, 256, "holes", "float32"),
+                       (256, 4, 64, 2048, 256, "skew", "float32"),
+                       (768, 4, 64, 256, 256, "random", "float32"),
+                       (1, 4, 64, 128, 128, None, "float32"),
+                       (20, 40, 64, 128, 128, "random", "float32"),
+                       (300, 1, 16, 128, 256, None, "bfloat16"),
+                       (1024, 4, 64, 256, 256, "ones", "float32"),
+                       (64, 8, 128, 256, 256, "random", "bfloat16")]
+
+
+@pytest.mark.parametrize("rows,top,experts,o,k,act,sdt", ROUTED_SWIGLU_CASES)
+def test_routed_fp8_expert_swiglu_is_its_kinds(dev, rows, top, experts, o, k, act, sdt):
+    """routed_fp8_expert_swiglu (the route scan inside the gate/up launch)
+    equals quantized_routes -> fp8_expert_swiglu: counts and the whole route
+    table (-1 padding included) exactly, the codes and scales of every routed
+    entry bit for bit.  Run twice into the same buffers."""
+    import torch
+    from akas_amd import ops
+
+    rng = np.random.default_rng(rows * 131 + experts)
+    ids = _distinct_ids(rng, rows, top, experts)
+    active = np.ones(rows, np.int32)
+    if act == "random":
+        active = (rng.random(rows) < 0.7).astype(np.int32)
+    elif act == "holes":
+        ids[rng.random((rows, top)) < 0.2] = -1
+        ids[0, 0] = experts  # outside the bank: never routed
+    elif act == "skew":
+        ids = np.stack([np.argsort(rng.random(experts - 1))[: top - 1] + 1 for _ in range(rows)])
+        ids = np.concatenate([np.zeros((rows, 1), np.int64), ids], axis=1).astype(np.int32)
+    x = random_codes(rng, (rows, k))
+    w = random_codes(rng, (experts, o, k))
+    w2 = random_codes(rng, (experts, o, k))
+    xs = rng.uniform(0.0625, 0.25, (rows, k // 128)).astype(np.float32)
+    ws = ofp8.bf16_round(rng.uniform(0.0625, 0.25, (experts, o // 128, k // 128)).astype(np.float32))
+    ws2 = ofp8.bf16_round(rng.uniform(0.0625, 0.25, (experts, o // 128, k // 128)).astype(np.float32))
+    S = getattr(torch, sdt)
+    dids, dact = _t(ids, dev), _t(active, dev)
+    data = [_t(x, dev), _t(xs, dev), _t(w, dev), _t(ws, dev, S), _t(w2, dev), _t(ws2, dev, S)]
+    bf = torch.bfloat16
+    counts, routes = ops.quantized_routes(dids, dact, experts=experts)
+    ecodes, escales = ops.fp8_expert_swiglu(*data, counts, routes, r=rows, top=top,
+                                            product_dtype=bf, activation_dtype=bf)
+    live = np.zeros((rows, top), bool)
+    hc, hr = _np(counts), _np(routes)
+    for e in range(experts):
+        for route in hr[e, :hc[e]]:
+            live[route // top, route % top] = True
+    outs = None
+    for _ in range(2):
+        outs = ops.routed_fp8_expert_swiglu(dids, None if act is None else dact, data[0], data[1],
+                                            *data[2:], product_dtype=bf, activation_dtype=bf,
+                                            **({} if outs is None else dict(
+                                                counts=outs[0], routes=outs[1], out=outs[2],
+                                                output_scales=outs[3])))
+        np.testing.assert_array_equal(_np(outs[0]), hc)
+        np.testing.assert_array_equal(_np(outs[1]), hr)
+        np.testing.assert_array_equal(_np(outs[2])[live], _np(ecodes)[live])
+        np.testing.assert_array_equal(_np(outs[3])[live], _np(escales)[live])
+    assert live.sum() == hc.sum() and hc.sum() > 0
+
+
+def test_routed_fp8_expert_swiglu_zero_rows(dev):
+    """An empty batch writes zero counts and launches no expert work."""
+    import torch
+    from akas_amd import ops
+
+    E, o, k = 8, 128, 128
+    w = torch.zeros((E, o, k), dtype=torch.uint8, device=dev)
+    s = torch.ones((E, 1, 1), dtype=torch.float32, device=dev)
+    counts = torch.full((E,), 7, dtype=torch.int32, device=dev)
+    out = ops.routed_fp8_expert_swiglu(
+        torch.zeros((0, 4), dtype=torch.int32, device=dev), None,
+        torch.zeros((0, k), dtype=torch.uint8, device=dev),
+        torch.zeros((0, 1), dtype=torch.float32, device=dev), w, s, w, s, counts=counts)
+    assert out[2].shape == (0, 4, o)
+    assert _np(counts).tolist() == [0] * E
+
+
+def test_routed_fp8_expert_swiglu_lfm2_decode(dev, lfm2_bank):
+    """The LFM2 decode layer's gate/up at its real size (T=256, 64 experts,
+    top 4, 2048 -> 1536, 768 workgroups three to a CU) from router ids:
+    the same tables and codes as the two kinds."""
+    import torch
+    from akas_amd import ops
+
+    wts, _ = lfm2_bank
+    rng = np.random.default_rng(5)
+    rows, H = 256, 2048
+    x = _t(bf16_normal(rng, (rows, H)), dev, torch.bfloat16)
+    logits = _t(rng.normal(0, 1, (rows, 64)).astype(np.float32), dev)
+    ids, _ = ops.biased_softmax_router(logits, torch.zeros(64, device=dev), top=4, scale=1.0)
+    codes, scales = ops.quantize(x)
+    active = torch.ones(rows, dtype=torch.int32, device=dev)
+    bf = torch.bfloat16
+    counts, routes = ops.quantized_routes(ids, active, experts=64)
+    ecodes, escales = ops.fp8_expert_swiglu(codes, scales, wts.w1, wts.s1, wts.w3, wts.s3, counts,
+                                            routes, r=rows, top=4, product_dtype=bf,
+                                            activation_dtype=bf)
+    c2, r2, codes2, scales2 = ops.routed_fp8_expert_swiglu(
+        ids, active, codes, scales, wts.w1, wts.s1, wts.w3, wts.s3, product_dtype=bf,
+        activation_dtype=bf)
+    assert torch.equal(c2, counts) and torch.equal(r2, routes)
+    assert torch.equal(codes2, ecodes) and torch.equal(scales2, escales)
+
+
 @pytest.mark.parametrize("rows", [33, 1200])
 def test_fused_swiglu_groups_holding_infinity(dev, rows):
     """Activations that overflow float16 (rows with large activation scales):
