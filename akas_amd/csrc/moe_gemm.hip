@@ -160,14 +160,29 @@ AKAS_DEV ExpertSlice expert_slice(const ExpertArgs& p, int e) {
 // in the activation buffer, clamped into the buffer (a corrupt route can
 // only misroute, never fault), and, when `live`, its scatter destination
 // (else -1).  The route is read once for both.
-AKAS_DEV void tile_row(const ExpertArgs& p, int e, int idx, bool live, int& src, int& dst) {
-  int route = 0, off = 0;
-  if (!p.packed_in || !p.packed_out) route = p.routes[(int64_t)e * p.r + idx];
-  if (p.packed_in || p.packed_out) off = p.offsets[e];
-  const int row = p.packed_in ? off + idx : (p.routed ? route : route / p.top);
+// tile_route issues the loads, tile_row_of uses them, so that loads issued
+// in between stay in flight.
+struct RowRoute {
+  int route, off;
+};
+
+AKAS_DEV RowRoute tile_route(const ExpertArgs& p, int e, int idx) {
+  RowRoute q{0, 0};
+  if (!p.packed_in || !p.packed_out) q.route = p.routes[(int64_t)e * p.r + idx];
+  if (p.packed_in || p.packed_out) q.off = p.offsets[e];
+  return q;
+}
+
+AKAS_DEV void tile_row_of(const ExpertArgs& p, RowRoute q, int idx, bool live, int& src,
+                          int& dst) {
+  const int row = p.packed_in ? q.off + idx : (p.routed ? q.route : q.route / p.top);
   src = row < 0 ? 0 : (row >= p.x_rows ? p.x_rows - 1 : row);
-  const int d = live ? (p.packed_out ? off + idx : route) : -1;
+  const int d = live ? (p.packed_out ? q.off + idx : q.route) : -1;
   dst = d < p.out_rows ? d : -1;
+}
+
+AKAS_DEV void tile_row(const ExpertArgs& p, int e, int idx, bool live, int& src, int& dst) {
+  tile_row_of(p, tile_route(p, e, idx), idx, live, src, dst);
 }
 
 // ---------------------------------------------------------------------------
@@ -490,20 +505,21 @@ void expert_tiled_kernel(ExpertArgs p) {
     }
     plan.dst0 = lds_off(row, ch);
   }
-  // With the route scan, the first weight k-block is requested before the
-  // scan's barriers, which then run under its latency.
-  if constexpr (SCAN) plan.fetch_b(kb0, rb);
-
-  // Gathered source rows and scatter destinations of this tile.
+  // Gathered source rows and scatter destinations of this tile.  The first
+  // weight k-block is requested before they are known: after the route
+  // loads, or before the route scan's barriers, which then run under it.
   if constexpr (SCAN) {
+    plan.fetch_b(kb0, rb);
     scan_tile_rows<BM>(p, sid, magic, e, row0, count, nb == 0, tid, scan_wave, rows_src,
                        rows_dst);
   } else {
-    for (int i = tid; i < BM; i += THREADS) {
-      const int idx = row0 + i;
-      const bool live = idx < count;
-      tile_row(p, e, live ? idx : row0, live, rows_src[i], rows_dst[i]);
-    }
+    static_assert(BM <= THREADS, "one tile row per thread");
+    const int idx = row0 + tid;
+    const bool live = idx < count;
+    RowRoute q{0, 0};
+    if (tid < BM) q = tile_route(p, e, live ? idx : row0);
+    plan.fetch_b(kb0, rb);
+    if (tid < BM) tile_row_of(p, q, live ? idx : row0, live, rows_src[tid], rows_dst[tid]);
   }
   __syncthreads();
 
@@ -528,10 +544,7 @@ void expert_tiled_kernel(ExpertArgs p) {
   float ras, rws0, rws1 = 0.f;
   if constexpr (NSTAGE == 1) {
     // one stage: stash, prefetch the next k-block, barrier, multiply, barrier
-    if constexpr (SCAN)
-      plan.fetch_a(kb0, ra);
-    else
-      plan.fetch(kb0, ra, rb);
+    plan.fetch_a(kb0, ra);
     ras = as_row[kb0];
     rws0 = load_scale_t<SDT>(xs.ws, ws_base + kb0);
     if constexpr (PAIRED) rws1 = load_scale_t<SDT>(xs.ws2, ws_base + kb0);
@@ -552,10 +565,7 @@ void expert_tiled_kernel(ExpertArgs p) {
     }
     __syncthreads();
   } else {
-    if constexpr (SCAN)
-      plan.fetch_a(kb0, ra);
-    else
-      plan.fetch(kb0, ra, rb);
+    plan.fetch_a(kb0, ra);
     ras = as_row[kb0];
     float ws0 = load_scale_t<SDT>(xs.ws, ws_base + kb0);
     float ws1 = PAIRED ? load_scale_t<SDT>(xs.ws2, ws_base + kb0) : 0.f;
