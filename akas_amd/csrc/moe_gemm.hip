@@ -1451,9 +1451,8 @@ extern "C" int akas_shared_expert_moe(
   float* act_scales = reinterpret_cast<float*>(base + L.act_scales);
   uint16_t* contributions = reinterpret_cast<uint16_t*>(base + L.contributions);
 
-  st = launch_decode_router(logits, ids, weights, r, experts, top, s);
-  if (st != AKAS_OK) return st;
-  st = launch_quantize(x, x_dtype, codes, scales, r, h, false, s);
+  st = launch_decode_router_quantize(logits, ids, weights, r, experts, top, x, x_dtype, codes,
+                                     scales, h, s);
   if (st != AKAS_OK) return st;
   launch_routes_with_shared(ids, counts, routes, r, experts, top, s);
 

@@ -7,10 +7,13 @@
 
 namespace akas {
 
-// decode_router (bf16-rounded logits, softmax over the top-k): ids and
-// weights [r, top].  Returns an AKAS status.
-int launch_decode_router(const float* logits, int32_t* ids, float* weights, int64_t r,
-                         int experts, int top, hipStream_t s);
+// decode_router (bf16-rounded logits, softmax over the top-k: ids and
+// weights [r, top]) and quantize of x [r, k] (x_dtype f32/f16/bf16) in one
+// launch: the same ids, weights, codes and scales as the two.  Returns an
+// AKAS status.
+int launch_decode_router_quantize(const float* logits, int32_t* ids, float* weights, int64_t r,
+                                  int experts, int top, const void* x, int x_dtype,
+                                  uint8_t* codes, float* scales, int64_t k, hipStream_t s);
 
 // quantized_routes: counts [experts] and routes [experts, r] from ids
 // [r, top] and active [r] (null: every row active).

@@ -72,15 +72,13 @@ constexpr int kMaxTop = 32;
 // its owner lane's registers (no load after the arg-max), and lane `rank`
 // keeps rank's value and id, so the top-k lives in registers without a
 // per-rank array.  Weights: the rank-ordered sums of the reference.
+// Rows 4 * block .. 4 * block + 3 (one per wave).
 template <int SOFTMAX, int SLOTS, int BF16>
-__global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ logits,
-                                                     const float* __restrict__ bias,
-                                                     int32_t* __restrict__ ids,
-                                                     float* __restrict__ weights, int64_t rows,
-                                                     int experts, int top, float scale,
-                                                     int normalize) {
+AKAS_DEV void router_rows(const float* __restrict__ logits, const float* __restrict__ bias,
+                          int32_t* __restrict__ ids, float* __restrict__ weights, int64_t rows,
+                          int experts, int top, float scale, int normalize, int block) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)block * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;  // uniform per wave
   const float* l = logits + row * experts;
   // base: the value a chosen expert contributes (the logit, or its sigmoid);
@@ -158,6 +156,17 @@ __global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ l
     ids[row * top + lane] = mine_id;
     weights[row * top + lane] = w;
   }
+}
+
+template <int SOFTMAX, int SLOTS, int BF16>
+__global__ __launch_bounds__(256) void router_kernel(const float* __restrict__ logits,
+                                                     const float* __restrict__ bias,
+                                                     int32_t* __restrict__ ids,
+                                                     float* __restrict__ weights, int64_t rows,
+                                                     int experts, int top, float scale,
+                                                     int normalize) {
+  router_rows<SOFTMAX, SLOTS, BF16>(logits, bias, ids, weights, rows, experts, top, scale,
+                                    normalize, blockIdx.x);
 }
 
 // experts <= 64 and top <= 8: four rows per wave, sixteen lanes per row (one
@@ -279,6 +288,27 @@ __global__ __launch_bounds__(256) void router_row16_kernel(const float* __restri
                               blockIdx.x);
 }
 
+// The quantizer half of a router + quantizer launch: workgroups from
+// `first_block` on quantize x row-major, 16 groups per workgroup and pass
+// (the quantizer's grid-stride loop and quantize8, so the codes are the
+// quantizer's).
+template <int DT>
+AKAS_DEV void quantize_tail(const void* __restrict__ x, uint8_t* __restrict__ codes,
+                            float* __restrict__ scales, int64_t groups, int first_block) {
+  const int lane16 = threadIdx.x & 15;
+  const int64_t qblocks = (int64_t)gridDim.x - first_block;
+  const int64_t first = (((int64_t)blockIdx.x - first_block) * blockDim.x + threadIdx.x) >> 4;
+  const int64_t stride = (qblocks * blockDim.x) >> 4;
+  for (int64_t g = first; g < groups; g += stride) {
+    const int64_t base = g * kBlock + lane16 * 8;
+    float v[8], sc;
+    load8<DT>(x, base, v);
+    const uint2 c = quantize8(v, sc);
+    *reinterpret_cast<uint2*>(codes + base) = c;
+    if (lane16 == 0) scales[g] = sc;
+  }
+}
+
 // The MoE block's router and its input quantizer in one launch: the first
 // router_blocks workgroups route 16 rows each (router_row16), the rest
 // quantize x row-major, 16 groups per workgroup and pass (the quantizer's
@@ -295,18 +325,27 @@ __global__ __launch_bounds__(256) void router_quantize_kernel(
                              blockIdx.x);
     return;
   }
-  const int lane16 = threadIdx.x & 15;
-  const int64_t qblocks = (int64_t)gridDim.x - router_blocks;
-  const int64_t first = (((int64_t)blockIdx.x - router_blocks) * blockDim.x + threadIdx.x) >> 4;
-  const int64_t stride = (qblocks * blockDim.x) >> 4;
-  for (int64_t g = first; g < groups; g += stride) {
-    const int64_t base = g * kBlock + lane16 * 8;
-    float v[8], sc;
-    load8<DT>(x, base, v);
-    const uint2 c = quantize8(v, sc);
-    *reinterpret_cast<uint2*>(codes + base) = c;
-    if (lane16 == 0) scales[g] = sc;
+  quantize_tail<DT>(x, codes, scales, groups, router_blocks);
+}
+
+// The shared-expert block's decode router (bf16-rounded logits, softmax over
+// the top-k, weights normalized) and its input quantizer in one launch, as
+// router_quantize_kernel: SLOTS 0 routes 16 rows per workgroup
+// (router_row16, up to 64 experts and top 8), else 4 (router_rows).
+template <int SLOTS, int DT>
+__global__ __launch_bounds__(256) void decode_router_quantize_kernel(
+    const float* __restrict__ logits, int32_t* __restrict__ ids, float* __restrict__ weights,
+    int64_t rows, int experts, int top, int router_blocks, const void* __restrict__ x,
+    uint8_t* __restrict__ codes, float* __restrict__ scales, int64_t groups) {
+  if ((int)blockIdx.x < router_blocks) {
+    if constexpr (SLOTS == 0)
+      router_row16<1, 1>(logits, nullptr, ids, weights, rows, experts, top, 1.0f, 1, blockIdx.x);
+    else
+      router_rows<1, SLOTS, 1>(logits, nullptr, ids, weights, rows, experts, top, 1.0f, 1,
+                               blockIdx.x);
+    return;
   }
+  quantize_tail<DT>(x, codes, scales, groups, router_blocks);
 }
 
 // ---------------------------------------------------------------------------
@@ -804,15 +843,40 @@ static int check_router(const float* logits, int32_t* ids, float* weights, int64
   return AKAS_OK;
 }
 
-// Launches of the shared-expert block (akas_shared_expert_moe), declared in
-// moe_launch.h; the arguments are checked by that entry point.
+// Launches run by the grouped expert kernels' entry points as well (declared
+// in moe_launch.h); the arguments are checked by the entry points.
 namespace akas {
 
-int launch_decode_router(const float* logits, int32_t* ids, float* weights, int64_t r,
-                         int experts, int top, hipStream_t s) {
+int launch_decode_router_quantize(const float* logits, int32_t* ids, float* weights, int64_t r,
+                                  int experts, int top, const void* x, int x_dtype,
+                                  uint8_t* codes, float* scales, int64_t k, hipStream_t s) {
   const int st = check_router(logits, ids, weights, r, experts, top);
   if (st != AKAS_OK || r == 0) return st;
-  launch_router<1, 1>(logits, nullptr, ids, weights, r, experts, top, 1.0f, 1, s);
+  if (k <= 0 || k % kBlock) return AKAS_ERR_GEOMETRY;
+  if (!x || !codes || !scales) return AKAS_ERR_NULL;
+  const bool row16 = experts <= 64 && top <= kRowTop;
+  const int64_t groups = r * (k / kBlock);
+  const int64_t rblocks = row16 ? (r + 15) / 16 : (r + 3) / 4, want = (groups + 15) / 16;
+  const int64_t qblocks = want < 8192 ? want : 8192;
+  if (rblocks + qblocks > 0x7FFFFFFF) return AKAS_ERR_GEOMETRY;
+  const dim3 grid((unsigned)(rblocks + qblocks));
+  auto go = [&](auto SL, auto XD) {
+    decode_router_quantize_kernel<decltype(SL)::value, decltype(XD)::value><<<grid, 256, 0, s>>>(
+        logits, ids, weights, r, experts, top, (int)rblocks, x, codes, scales, groups);
+  };
+  auto by_x = [&](auto SL) {
+    switch (x_dtype) {
+      case AKAS_DTYPE_F32: go(SL, DtypeTag<AKAS_DTYPE_F32>{}); break;
+      case AKAS_DTYPE_F16: go(SL, DtypeTag<AKAS_DTYPE_F16>{}); break;
+      default: go(SL, DtypeTag<AKAS_DTYPE_BF16>{});
+    }
+  };
+  if (row16)
+    by_x(DtypeTag<0>{});
+  else if (experts <= 256)
+    by_x(DtypeTag<4>{});
+  else
+    by_x(DtypeTag<kMaxExpertSlots>{});
   return AKAS_OK;
 }
 

@@ -494,7 +494,8 @@ int akas_routed_combine(const void* experts, int input_dtype, const float* weigh
  * moe_combine (cuda.py:392-422).  For callers that run the whole block: the
  * shared expert (sw1/sw3 [f, h], sw2 [h, f], scales as the bank's) is
  * computed as expert `experts` of the routed launches, at rank top of every
- * row, so the block takes six launches and no dense launches beside them.
+ * row, and the router shares a launch with the quantizer of x, so the block
+ * takes five launches and no dense launches beside them.
  * Bank w1/w3 [experts, f, h], w2 [experts, h, f], 128x128 block scales of
  * scale_dtype (f32 or bf16) for all six weights.  Contributions are kept in
  * bf16, which moe_combine rounds them to.  h % 128 == 0, f % 128 == 0,
