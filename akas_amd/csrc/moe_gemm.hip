@@ -54,6 +54,9 @@ struct ExpertArgs {
   const int32_t* active;    // [r] or null (every row active)
   int32_t* scan_counts;     // SCAN: counts [E] written for the later launches
   int32_t* scan_routes;     // SCAN: routes [E, r] written for the later launches
+  // SCAN: columns of ids.  Below top, expert E-1 is the shared expert, routed
+  // by every row at rank scan_cols, and ids name experts 0 .. E-2.
+  int scan_cols;
   float* cout;              // [r, N] f32 combined rows
   int32_t* arrivals;        // [r, N / BN] per (row, column block) arrival counts
   int r, top, E, N, K;
@@ -188,51 +191,84 @@ AKAS_DEV void tile_row(const ExpertArgs& p, int e, int idx, bool live, int& src,
 // ---------------------------------------------------------------------------
 // The route scan fused into the decode gate/up launch (quantized_routes,
 // src/akas/ops/moe/kernel.py:121-151, done by every workgroup for itself).
-// Up to 64 experts and 4096 (row, rank) entries f = row * top + rank of ids
-// [r, top]: thread t of the 256 holds entries t + 256j, so each pass j reads
-// 1 KB of ids in one coalesced load per wave (every workgroup of the launch
-// reads the same lines; per-lane strided loads cost the launch 6 us).  An
-// expert's route at position q is its q-th live entry in f order; counts[e]
-// = min(entries, r), as the route tables hold at most r routes per expert.
+// Up to 512 experts and 4096 entries g = row * cols + rank of ids [r, cols]
+// (cols = scan_cols): thread t of the 256 holds entries t + 256j, so each
+// pass j reads 1 KB of ids in one coalesced load per wave (every workgroup of
+// the launch reads the same lines; per-lane strided loads cost the launch
+// 6 us).  An expert's route at position q is its q-th live entry in g order,
+// and names the entry row * top + rank; counts[e] = min(entries, r), as the
+// route tables hold at most r routes per expert.  With a shared expert
+// (cols < top), expert E-1 routes every row at rank cols, in row order.
 // ---------------------------------------------------------------------------
 constexpr int kScanThreads = 256;
 constexpr int kScanPasses = 16;
 constexpr int kScanMaxEntries = kScanThreads * kScanPasses;
-constexpr int kScanMaxExperts = 64;
-constexpr int kScanMaxTop = 64;
+constexpr int kScanMaxExperts = 512;
+constexpr int kScanMaxCols = 64;
 
-// Row of entry f (f < 65536, top <= 64): the high word of f * ceil(2^32/top)
-// equals f / top over that whole range (checked exhaustively).
-AKAS_DEV int scan_row(int f, uint32_t magic) {
-  return magic ? (int)__umulhi((uint32_t)f, magic) : f;
+// Row of entry g (g < 65536, cols <= 64): the high word of g * ceil(2^32/cols)
+// equals g / cols over that whole range (checked exhaustively).
+AKAS_DEV int scan_row(int g, uint32_t magic) {
+  return magic ? (int)__umulhi((uint32_t)g, magic) : g;
+}
+
+// The route naming entry g: row * top + rank.
+AKAS_DEV int scan_route(const ExpertArgs& p, int g, int row) {
+  return g + row * (p.top - p.scan_cols);
 }
 
 // Entry t + 256j of this thread: its expert id, or -1 past the end, for an
-// inactive row or an id outside 0 .. E-1.  Every load is issued before the
-// first is used.
+// inactive row or an id outside the routed experts.  Every load is issued
+// before the first is used.
 AKAS_DEV void scan_entries(const ExpertArgs& p, int tid, uint32_t magic, int (&id)[kScanPasses]) {
-  const int n = p.r * p.top;
+  const int n = p.r * p.scan_cols;
+  const unsigned routed = (unsigned)(p.scan_cols < p.top ? p.E - 1 : p.E);
   int raw[kScanPasses], act[kScanPasses];
 #pragma unroll
   for (int j = 0; j < kScanPasses; ++j) {
-    const int f = tid + kScanThreads * j;
+    const int g = tid + kScanThreads * j;
     raw[j] = -1;
     act[j] = 1;
-    if (f < n) {
-      raw[j] = p.ids[f];
-      if (p.active) act[j] = p.active[scan_row(f, magic)];
+    if (g < n) {
+      raw[j] = p.ids[g];
+      if (p.active) act[j] = p.active[scan_row(g, magic)];
     }
   }
 #pragma unroll
   for (int j = 0; j < kScanPasses; ++j)
-    id[j] = ((act[j] != 0) & ((unsigned)raw[j] < (unsigned)p.E)) ? raw[j] : -1;
+    id[j] = ((act[j] != 0) & ((unsigned)raw[j] < routed)) ? raw[j] : -1;
+}
+
+// find_item over the counts in LDS (hist, capped at r).
+AKAS_DEV bool find_item_hist(const int* hist, int experts, int r, int bm, int tiles_n, int lane,
+                             Item& it) {
+  if (experts <= 64)
+    return find_item_64(lane < experts ? min(hist[lane], r) : 0, r, bm, tiles_n, lane, it);
+  int total = 0;
+  for (int e0 = 0; e0 < experts; e0 += 64) {
+    const int e = e0 + lane;
+    total += wave_sum_i(e < experts ? (min(hist[e], r) + bm - 1) / bm : 0);
+  }
+  const int items = total * tiles_n;
+  const int id = xcd_remap(blockIdx.x, items);
+  if (id >= items) return false;
+  it.nb = id % tiles_n;
+  const int t = id / tiles_n;
+  int base = 0;
+  for (int e0 = 0; e0 < experts; e0 += 64) {
+    const int e = e0 + lane;
+    const int c = e < experts ? min(hist[e], r) : 0;
+    if (tile_in_chunk((c + bm - 1) / bm, c, e0, t, r, lane, base, it)) return true;
+  }
+  return false;  // not reached: t < total
 }
 
 // counts [E] (workgroup 0) and the -1 padding of routes [E, r] past each
 // expert's count (expert e by workgroup e, e + grid, ...): the tables
 // quantized_routes leaves, for the launches after this one.
 AKAS_DEV void scan_tables(const ExpertArgs& p, const int* hist, int tid) {
-  if (blockIdx.x == 0 && tid < p.E) p.scan_counts[tid] = min(hist[tid], p.r);
+  if (blockIdx.x == 0)
+    for (int e = tid; e < p.E; e += kScanThreads) p.scan_counts[e] = min(hist[e], p.r);
   for (int e = blockIdx.x; e < p.E; e += gridDim.x) {
     int32_t* out = p.scan_routes + (int64_t)e * p.r;
     for (int i = min(hist[e], p.r) + tid; i < p.r; i += kScanThreads) out[i] = -1;
@@ -248,6 +284,18 @@ template <int BM>
 AKAS_DEV void scan_tile_rows(const ExpertArgs& p, const int (&id)[kScanPasses], uint32_t magic,
                              int e, int row0, int count, bool write_routes, int tid,
                              int (*wave_count)[4], int* rows_src, int* rows_dst) {
+  int32_t* routes = p.scan_routes + (int64_t)e * p.r;
+  if (p.scan_cols < p.top && e == p.E - 1) {  // the shared expert (uniform)
+    if (tid < BM) {
+      const int pos = row0 + tid;
+      const bool live = pos < count;
+      const int route = pos * p.top + p.scan_cols;
+      rows_src[tid] = live ? pos : row0;
+      rows_dst[tid] = live ? route : -1;
+      if (live && write_routes) routes[pos] = route;
+    }
+    return;
+  }
   const int lane = tid & 63, wave = tid >> 6;
   const uint64_t below = (uint64_t{1} << lane) - 1;
   uint64_t hit[kScanPasses];
@@ -260,7 +308,6 @@ AKAS_DEV void scan_tile_rows(const ExpertArgs& p, const int (&id)[kScanPasses], 
     wave_count[lane][wave] = __builtin_popcountll(h);
   }
   __syncthreads();
-  int32_t* routes = p.scan_routes + (int64_t)e * p.r;
   int done = 0;  // matches in the passes before j
 #pragma unroll
   for (int j = 0; j < kScanPasses; ++j) {
@@ -269,8 +316,9 @@ AKAS_DEV void scan_tile_rows(const ExpertArgs& p, const int (&id)[kScanPasses], 
     const int before = (wave > 0 ? c0 : 0) + (wave > 1 ? c1 : 0) + (wave > 2 ? c2 : 0);
     const int pos = done + before + __builtin_popcountll(hit[j] & below);
     if ((id[j] == e) & (pos >= row0) & (pos < row0 + BM) & (pos < count)) {
-      const int f = tid + kScanThreads * j;
-      const int src = scan_row(f, magic);
+      const int g = tid + kScanThreads * j;
+      const int src = scan_row(g, magic);
+      const int f = scan_route(p, g, src);
       rows_src[pos - row0] = src;
       rows_dst[pos - row0] = f;
       if (write_routes) routes[pos] = f;
@@ -452,14 +500,15 @@ void expert_tiled_kernel(ExpertArgs p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if constexpr (MODE == kCombine) zero_unrouted_rows<THREADS>(p);
   int sid[SCAN ? kScanPasses : 1];
-  const uint32_t magic = p.top > 1 ? 0xFFFFFFFFu / (uint32_t)p.top + 1u : 0u;
+  const uint32_t magic = p.scan_cols > 1 ? 0xFFFFFFFFu / (uint32_t)p.scan_cols + 1u : 0u;
   if constexpr (SCAN) {
     scan_entries(p, tid, magic, sid);
-    if (tid < kScanMaxExperts) scan_hist[tid] = 0;
+    for (int e = tid; e < p.E; e += THREADS) scan_hist[e] = 0;
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < kScanPasses; ++j)
       if (sid[j] >= 0) atomicAdd(&scan_hist[sid[j]], 1);
+    if (p.scan_cols < p.top && tid == 0) scan_hist[p.E - 1] = p.r;  // the shared expert
     __syncthreads();
     scan_tables(p, scan_hist, tid);
   }
@@ -471,8 +520,7 @@ void expert_tiled_kernel(ExpertArgs p) {
   // block 190.5 -> 183.2 us against tiles fastest over the whole grid).
   Item item;
   if constexpr (SCAN) {
-    const int c = lane < p.E ? min(scan_hist[lane], p.r) : 0;
-    if (!find_item_64(c, p.r, BM, p.tiles_n, lane, item)) return;  // uniform
+    if (!find_item_hist(scan_hist, p.E, p.r, BM, p.tiles_n, lane, item)) return;  // uniform
   } else if (!find_item(p.counts, p.E, p.r, BM, p.tiles_n, lane, item)) {
     return;  // uniform
   }
@@ -1051,12 +1099,12 @@ static void launch_swiglu(const ExpertArgs& a, hipStream_t s) {
 }
 
 // Shapes the fused route scan covers: a decode batch's routes (at least one
-// row, up to 4096 entries, at most 48 per expert on average, top <= 64) over
-// up to 64 experts.
-static bool scan_fits(int64_t r, int top, int experts) {
-  const int64_t n = r * top;
-  return r >= 1 && top <= kScanMaxTop && experts <= kScanMaxExperts && n <= kScanMaxEntries &&
-         n / experts <= 48;
+// row, up to 4096 entries of ids [r, cols], cols <= 64, at most 48 routes per
+// expert on average over the launch's top ranks) over up to 512 experts.
+static bool scan_fits(int64_t r, int cols, int top, int experts) {
+  const int64_t n = r * cols;
+  return r >= 1 && cols <= kScanMaxCols && experts <= kScanMaxExperts &&
+         n <= kScanMaxEntries && r * top / experts <= 48;
 }
 
 static inline bool float_dtype(int d) {
@@ -1221,12 +1269,13 @@ extern "C" int akas_routed_fp8_expert_swiglu(
   a.x = x; a.as = activation_scales; a.w = w; a.ws = w_scales; a.w2 = w2; a.ws2 = w2_scales;
   a.counts = counts; a.routes = routes;
   a.ids = ids; a.active = active; a.scan_counts = counts; a.scan_routes = routes;
+  a.scan_cols = top;
   a.out = out; a.out_scales = output_scales;
   a.r = (int)r; a.top = top; a.E = experts; a.N = (int)o; a.K = (int)k;
   a.x_rows = (int)r; a.out_rows = (int)(r * top);
   a.parts = 1; a.kb_per_part = (int)(k / kBlock);
   a.ws_dtype = scale_dtype; a.prod_dtype = product_dtype; a.act_dtype = activation_dtype;
-  if (scan_fits(r, top, experts)) {
+  if (scan_fits(r, top, top, experts)) {
     launch_paired<kSwigluFp8, AKAS_DTYPE_F32, 1>(a, s);
   } else {
     launch_quantized_routes(ids, active, counts, routes, r, experts, top, s);
@@ -1454,8 +1503,6 @@ extern "C" int akas_shared_expert_moe(
   st = launch_decode_router_quantize(logits, ids, weights, r, experts, top, x, x_dtype, codes,
                                      scales, h, s);
   if (st != AKAS_OK) return st;
-  launch_routes_with_shared(ids, counts, routes, r, experts, top, s);
-
   ExpertArgs g{};
   g.x = codes; g.as = scales; g.w = w1; g.ws = s1; g.w2 = w3; g.ws2 = s3;
   g.xw = sw1; g.xws = ss1; g.xw2 = sw3; g.xws2 = ss3;
@@ -1464,7 +1511,16 @@ extern "C" int akas_shared_expert_moe(
   g.x_rows = (int)r; g.out_rows = (int)ranks;
   g.parts = 1; g.kb_per_part = (int)(h / kBlock);
   g.ws_dtype = scale_dtype; g.prod_dtype = AKAS_DTYPE_F32; g.act_dtype = AKAS_DTYPE_F32;
-  launch_swiglu(g, s);
+  // Decode batches scan the routes inside the gate/up launch (counts and
+  // routes as launch_routes_with_shared leaves them); larger ones take the
+  // route scan's own launch.
+  if (scan_fits(r, top, top + 1, experts + 1)) {
+    g.ids = ids; g.scan_counts = counts; g.scan_routes = routes; g.scan_cols = top;
+    launch_paired<kSwigluFp8, AKAS_DTYPE_F32, 1>(g, s);
+  } else {
+    launch_routes_with_shared(ids, counts, routes, r, experts, top, s);
+    launch_swiglu(g, s);
+  }
 
   ExpertArgs d{};
   d.x = act; d.as = act_scales; d.w = w2; d.ws = s2; d.xw = sw2; d.xws = ss2;

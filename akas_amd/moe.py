@@ -314,8 +314,8 @@ def shared_expert_moe(x, logits, shared_gate, weights: ExpertWeights, shared: Sh
     ``shared_as_expert``: with the default routes, fused SwiGLU, unpacked
     rows, a shared expert as wide as the routed ones and one scale dtype, the
     block is ``ops.shared_expert_moe_block``: the shared expert is one more
-    expert of the routed launches (rank ``top`` of every row), five launches
-    in all.  Otherwise, or with ``shared_as_expert=False``, the shared expert
+    expert of the routed launches (rank ``top`` of every row), four launches
+    in all for decode batches.  Otherwise, or with ``shared_as_expert=False``, the shared expert
     runs as dense FP8 linears on a second stream beside the routed experts.
     (64 tokens, 256 experts, top 8, H 2048, F 512: 180-181 us with the
     second stream; 168 us without any shared expert.)

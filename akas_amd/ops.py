@@ -745,8 +745,8 @@ def routed_fp8_expert_swiglu(ids, active, x, activation_scales, w, scales, w2, s
     call: ``(counts, routes, out, output_scales)``, each bit-identical to the
     two kinds run in turn (src/akas/ops/moe/kernel.py:121-151,
     src/akas/ops/moe/cuda.py:823-946).  ``active`` may be None (every row
-    active).  Decode batches (up to 64 experts, 4096 routes, 48 per expert on
-    average) take one launch, in which every workgroup scans ``ids`` itself.
+    active).  Decode batches (up to 512 experts, top 64, 4096 routes, 48 per expert
+    on average) take one launch, in which every workgroup scans ``ids`` itself.
     """
     _need(ids, "ids", torch.int32)
     r, top = ids.shape

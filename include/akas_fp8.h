@@ -391,7 +391,7 @@ int akas_fp8_expert_swiglu(const uint8_t* x, const float* activation_scales, con
  * akas_quantized_routes' (the down projection and the combine read them),
  * out u8 [r, top, o] and output_scales f32 [r, top, o/128] to
  * akas_fp8_expert_swiglu's over those tables.  active [r] may be null
- * (every row active).  One launch when experts <= 64, 1 <= r*top <= 4096 and
+ * (every row active).  One launch when experts <= 512, top <= 64, 1 <= r*top <= 4096 and
  * r*top / experts <= 48 (every workgroup scans ids itself); otherwise the two
  * kinds' launches.
  */
@@ -494,8 +494,9 @@ int akas_routed_combine(const void* experts, int input_dtype, const float* weigh
  * moe_combine (cuda.py:392-422).  For callers that run the whole block: the
  * shared expert (sw1/sw3 [f, h], sw2 [h, f], scales as the bank's) is
  * computed as expert `experts` of the routed launches, at rank top of every
- * row, and the router shares a launch with the quantizer of x, so the block
- * takes five launches and no dense launches beside them.
+ * row, the router shares a launch with the quantizer of x and, for decode
+ * batches, the route scan runs inside the gate/up launch: four launches and
+ * no dense launches beside them.
  * Bank w1/w3 [experts, f, h], w2 [experts, h, f], 128x128 block scales of
  * scale_dtype (f32 or bf16) for all six weights.  Contributions are kept in
  * bf16, which moe_combine rounds them to.  h % 128 == 0, f % 128 == 0,

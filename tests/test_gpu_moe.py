@@ -490,8 +490,8 @@ def _distinct_ids(rng, rows, top, experts):
 # (rows, top, experts, o, k, active, scale dtype): one launch (16-row tiles at
 # up to 8 routes per expert, the one-round and the two-stage 32-row tiles,
 # rows past a 16-entry boundary, inactive rows, ids outside the bank, one
-# expert taking every row) and the two-launch shapes (4096 routes at 64 per
-# expert, 128 experts)
+# expert taking every row, more than 64 and more than 256 experts) and the
+# two-launch shapes (4096 routes at 64 per expert, 8192 routes)
 ROUTED_SWIGLU_CASES = [(256, 4, 64, 256, 512, "ones", "float32"),
                        (8, 4, 64, 256, 256, "ones", "bfloat16"),
                        (3, 2, 8, 128, 256, None, "float32"),
@@ -503,7 +503,9 @@ ROUTED_SWIGLU_CASES = [(256, 4, 64, 256, 512, "ones", "float32"),
                        (20, 40, 64, 128, 128, "random", "float32"),
                        (300, 1, 16, 128, 256, None, "bfloat16"),
                        (1024, 4, 64, 256, 256, "ones", "float32"),
-                       (64, 8, 128, 256, 256, "random", "bfloat16")]
+                       (64, 8, 128, 256, 256, "random", "bfloat16"),
+                       (40, 8, 300, 128, 256, "holes", "bfloat16"),
+                       (1024, 8, 256, 128, 128, "random", "float32")]
 
 
 @pytest.mark.parametrize("rows,top,experts,o,k,act,sdt", ROUTED_SWIGLU_CASES)
