@@ -1610,15 +1610,18 @@ def test_shared_expert_moe_block_graph_replays(dev, shared_as_expert):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("rows", [64, 300])
 @pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("fused_combine", [False, True])
-def test_routed_moe_layer_graph_replays(dev, packed, fused_combine):
+def test_routed_moe_layer_graph_replays(dev, packed, fused_combine, rows):
     """The routed block captured in a HIP graph: every replay (with eager work
-    and synchronizations between them) equals the eager result."""
+    and synchronizations between them) equals the eager result.  Unpacked, 64
+    rows take the route scan inside the gate/up launch (16 routes per expert),
+    300 rows its own launch (75 per expert)."""
     import torch
     from akas_amd import moe
 
-    rows, H, F, E, top = 300, 512, 256, 16, 4
+    H, F, E, top = 512, 256, 16, 4
     rng = np.random.default_rng(98)
     bank = {}
     for name, shape in (("w1", (E, F, H)), ("w3", (E, F, H)), ("w2", (E, H, F))):
