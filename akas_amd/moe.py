@@ -89,7 +89,8 @@ class SharedExpert:
 
 def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed, max_block_m,
                           product_dtype, activation_dtype, contribution_dtype, quantized=None,
-                          partitions=1, combine_weights=None, separate_quantize=False):
+                          partitions=1, combine_weights=None, separate_quantize=False,
+                          every_row_active=False):
     """Routes, FP8 activations and the grouped expert products:
     ``[T, top, H]`` contributions in ``contribution_dtype``.  ``quantized``:
     x's codes and scales when the caller made them already.  ``partitions``
@@ -109,8 +110,10 @@ def _expert_contributions(x, ids, active, weights, *, top, fused_swiglu, packed,
     # (one launch fewer per decode layer, the same tables and codes).
     routed_gate_up = fused_swiglu and not packed and not separate_quantize and partitions == 1
     if routed_gate_up:
+        # every_row_active: active is the all-ones mask, which the scan then
+        # need not read
         counts, routes, act, act_scales = ops.routed_fp8_expert_swiglu(
-            ids, active, codes, scales, weights.w1, weights.s1, weights.w3, weights.s3,
+            ids, None if every_row_active else active, codes, scales, weights.w1, weights.s1, weights.w3, weights.s3,
             product_dtype=product_dtype, activation_dtype=activation_dtype)
     else:
         counts, routes = ops.quantized_routes(ids, active, experts=experts)
@@ -241,7 +244,8 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
         # as the reference's seed combining "partitions: 2" with "packed:
         # True" runs (:637-652).
         partitions = 1
-    if active is None:
+    every_row_active = active is None
+    if every_row_active:
         active = _all_active(rows, x.device)
     quantized = None
     if weights.experts <= 64 and top <= 8 and x.shape[1] % ops.BLOCK == 0:
@@ -261,7 +265,7 @@ def routed_moe(x, logits, bias, weights: ExpertWeights, *, top, active=None,
         activation_dtype=activation_dtype, contribution_dtype=contribution_dtype,
         quantized=quantized, partitions=partitions,
         combine_weights=probability if fused_combine and partitions == 1 else None,
-        separate_quantize=separate_quantize)
+        separate_quantize=separate_quantize, every_row_active=every_row_active)
     if out is None:
         out = ops.routed_combine(contributions, probability, active)
     if return_routing:
@@ -352,7 +356,8 @@ def shared_expert_moe(x, logits, shared_gate, weights: ExpertWeights, shared: Sh
         contributions, _, _, _ = _expert_contributions(
             x, ids, _all_active(rows, x.device), weights, top=top, fused_swiglu=fused_swiglu,
             packed=packed, max_block_m=max_block_m, product_dtype=torch.float32,
-            activation_dtype=torch.float32, contribution_dtype=contribution_dtype)
+            activation_dtype=torch.float32, contribution_dtype=contribution_dtype,
+            every_row_active=True)
     main.wait_stream(side)
     shared_out.record_stream(main)  # made on the side stream, read on this one
     return ops.moe_combine(contributions, probability, shared_out, shared_gate)
